@@ -1,0 +1,315 @@
+"""CPU oracle for the MTP verify step: numpy + the C restatement in cubic_oracle.c.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker (or the timed CPU baseline).  Product code never imports it.
+
+Reference paths are relative to ``src/cubic_serve/`` of QuantTrio/cubic-serve.
+
+Function                  restates                                         pinned by
+------------------------  -----------------------------------------------  ------------------------------
+unpack_cubic              quantization/extensions/cubic/reference.py:31-47  all-codes KAT (tests/ops/test_quantization_reference.py:136-152), brute-force bit loop
+pack_cubic                inverse of the above (fixture helper)             round trip with unpack_cubic
+cubic_metadata            reference.py:50-95                                KATs [[1,1],[6,6]] (:154-171) and ones(4,2) (:173-186)
+decode_cubic              reference.py:98-121                               closed form at t in {0,1}; fl32(m/D) exactness; KATs above
+linear_bf16               ops/eager/linear.py:43-56 + quantization.py:181  FP64 anchor + enclosure bound
+check_linear_enclosure    guardrail/quantization.py:176-320                 closed form; rejects a +0.25 corruption
+candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows
+verify_k1                 ops/cuda/sampling/speculative.py:46-219           reference KATs :73-131, :230-309; frozen-draw sweep :133-228; double-precision _oracle
+merge_prefix              executor/draft_graph.py:146-157                   chain KATs tests/generation/test_tp_sampling.py:120-178
+philox_uniform            guardrail/quantized_graph/speculative.py:15-30    Random123 Philox4x32-10 known-answer vectors
+expf                      (build-fixed exp for the acceptance transform)    <= 2 ulp against libm expf over a dense sweep
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "_build" / "libcubic_oracle.so"
+_lib = None
+
+METADATA_FORMATS = (
+    "float32-scale-float16-ab",
+    "int8-scale-int4-ab-global-fp32",
+    "e5m9-scale-curve2-tensor-fp16",
+)
+
+
+def build() -> Path:
+    """Compile the C restatement (gcc, -ffp-contract=off) into oracle/_build/."""
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        _lib.oracle_expf.restype = ctypes.c_float
+        _lib.oracle_expf.argtypes = [ctypes.c_float]
+        _lib.oracle_philox_uniform.restype = ctypes.c_float
+        _lib.oracle_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        _lib.oracle_half_to_float.restype = ctypes.c_float
+        _lib.oracle_half_to_float.argtypes = [ctypes.c_uint16]
+        _lib.oracle_float_to_half.restype = ctypes.c_uint16
+        _lib.oracle_float_to_half.argtypes = [ctypes.c_float]
+        _lib.oracle_float_to_bf16.restype = ctypes.c_uint16
+        _lib.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=dtype)
+
+
+# --------------------------------------------------------------------------- #
+# bf16 helpers (numpy has no bfloat16: carry raw uint16 bit patterns)
+# --------------------------------------------------------------------------- #
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_round_bf16(_p(x), _p(out), ctypes.c_int64(x.size))
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (_c(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def expf(x: float) -> float:
+    return lib().oracle_expf(float(x))
+
+
+def philox_uniform(seed: int, ordinal: int) -> float:
+    return lib().oracle_philox_uniform(seed & (2**64 - 1), ordinal & (2**64 - 1))
+
+
+def philox4x32_10(counter, key) -> list[int]:
+    c = (ctypes.c_uint32 * 4)(*counter)
+    k = (ctypes.c_uint32 * 2)(*key)
+    out = (ctypes.c_uint32 * 4)()
+    lib().oracle_philox4x32_10(c, k, out)
+    return list(out)
+
+
+# --------------------------------------------------------------------------- #
+# A1-A3: Cubic bitstream, metadata and decode
+# --------------------------------------------------------------------------- #
+def unpack_cubic(packed: np.ndarray, bits: int, input_size: int) -> np.ndarray:
+    packed = _c(packed, np.uint8)
+    rows = packed.shape[0]
+    if packed.shape[1] != math.ceil(input_size * bits / 8):
+        raise ValueError("Cubic packed row length does not match logical K")
+    out = np.empty((rows, input_size), np.int8)
+    rc = lib().oracle_unpack_cubic(_p(packed), ctypes.c_int64(rows), ctypes.c_int64(input_size),
+                                   ctypes.c_int(bits), _p(out))
+    if rc:
+        raise ValueError("invalid bit width")
+    return out
+
+
+def pack_cubic(codes: np.ndarray, bits: int) -> np.ndarray:
+    codes = _c(codes, np.int8)
+    rows, k = codes.shape
+    out = np.empty((rows, math.ceil(k * bits / 8)), np.uint8)
+    lib().oracle_pack_cubic(_p(codes), ctypes.c_int64(rows), ctypes.c_int64(k), ctypes.c_int(bits),
+                            _p(out))
+    return out
+
+
+def _group_partitions(n: int, group_out: int, partitions) -> np.ndarray:
+    parts = tuple(partitions) if partitions else (n,)
+    if sum(parts) != n or any(p <= 0 or p % group_out for p in parts):
+        raise ValueError("Cubic output partitions must preserve output-group boundaries")
+    return np.repeat(np.arange(len(parts), dtype=np.int32), [p // group_out for p in parts])
+
+
+def cubic_metadata(payload: dict, metadata: str, shape, group_in: int, group_out: int = 1,
+                   partitions=()):
+    """Expanded per-group (scale f32, a f16 bits, b f16 bits); reference.py:50-95."""
+    n, k = shape
+    grows, gcols = n // group_out, math.ceil(k / group_in)
+    if metadata == METADATA_FORMATS[0]:
+        return (_c(payload["weight_scale"], np.float32).reshape(grows, gcols),
+                _c(payload["weight_a"], np.float16).view(np.uint16).reshape(grows, gcols),
+                _c(payload["weight_b"], np.float16).view(np.uint16).reshape(grows, gcols))
+    parts = _group_partitions(n, group_out, partitions)
+    s = np.empty((grows, gcols), np.float32)
+    a = np.empty((grows, gcols), np.uint16)
+    b = np.empty((grows, gcols), np.uint16)
+    if metadata == METADATA_FORMATS[1]:
+        lib().oracle_metadata_fmt1(
+            _p(_c(payload["weight_scale"], np.int8)), _p(_c(payload["weight_ab"], np.uint8)),
+            _p(_c(payload["weight_scale_global"], np.float32)),
+            _p(_c(payload["weight_a_global"], np.float32)),
+            _p(_c(payload["weight_b_global"], np.float32)), _p(parts),
+            ctypes.c_int64(grows), ctypes.c_int64(gcols), _p(s), _p(a), _p(b))
+    elif metadata == METADATA_FORMATS[2]:
+        lib().oracle_metadata_fmt2(
+            _p(_c(payload["weight_metadata"], np.uint16)),
+            _p(_c(payload["weight_curve_a"], np.float16).view(np.uint16)),
+            _p(_c(payload["weight_curve_b"], np.float16).view(np.uint16)), _p(parts),
+            ctypes.c_int64(grows), ctypes.c_int64(gcols), _p(s), _p(a), _p(b))
+    else:
+        raise ValueError(f"unsupported Cubic metadata {metadata!r}")
+    return s, a, b
+
+
+def decode_cubic(payload: dict, bits: int, metadata: str, shape, group_in: int,
+                 group_out: int = 1, partitions=()) -> np.ndarray:
+    """FP32 decoded weights [N, K]; reference.py:98-121."""
+    n, k = shape
+    codes = unpack_cubic(payload["weight_packed"], bits, k)
+    s, a, b = cubic_metadata(payload, metadata, shape, group_in, group_out, partitions)
+    if not np.isfinite(s).all() or (s < 0).any():
+        raise ValueError("Cubic decoded scale must be finite and nonnegative")
+    w = np.empty((n, k), np.float32)
+    lib().oracle_decode_cubic(_p(codes), _p(s), _p(a), _p(b), ctypes.c_int64(n), ctypes.c_int64(k),
+                              ctypes.c_int(bits), ctypes.c_int64(group_in),
+                              ctypes.c_int64(group_out), _p(w))
+    return w
+
+
+def decode_bf16(payload: dict, bits: int, metadata: str, shape, group_in: int,
+                group_out: int = 1, partitions=()) -> np.ndarray:
+    """Decoded weights rounded once to bf16 (raw uint16 bits), as the WNA16 path
+    does before its FP32 dot (ops/eager/quantization.py:181-182)."""
+    return f32_to_bf16_bits(decode_cubic(payload, bits, metadata, shape, group_in, group_out,
+                                         partitions))
+
+
+# --------------------------------------------------------------------------- #
+# A5/A6: reference linear and its FP64 enclosure
+# --------------------------------------------------------------------------- #
+def linear_bf16(x_bits: np.ndarray, w_bits: np.ndarray):
+    """y = bf16(sum_k fp32(x) * fp32(w)), ascending k; returns (y bf16 bits, y fp32)."""
+    x_bits, w_bits = _c(x_bits, np.uint16), _c(w_bits, np.uint16)
+    m, k = x_bits.shape
+    n = w_bits.shape[0]
+    y = np.empty((m, n), np.uint16)
+    y32 = np.empty((m, n), np.float32)
+    lib().oracle_linear_bf16(_p(x_bits), ctypes.c_int64(m), ctypes.c_int64(k), _p(w_bits),
+                             ctypes.c_int64(n), _p(y), _p(y32))
+    return y, y32
+
+
+def check_linear_enclosure(x_bits: np.ndarray, w_bits: np.ndarray, y_bits: np.ndarray) -> dict:
+    """guardrail/quantization.py:250-320 for a bf16 boundary.
+
+    |y - x.w|_f64 <= sum|x||w| (g32 + g64)/(1 - g64) (1 + u) + |anchor| u + tiny*u
+    with g32 = s 2^-24 / (1 - s 2^-24), s = k + 12, g64 = k 2^-53 / (1 - k 2^-53),
+    u = eps(bf16)/2.  Raises AssertionError on any excess, like the reference.
+    """
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    w = bf16_bits_to_f32(w_bits).astype(np.float64)
+    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    k = x.shape[1]
+    if not (np.isfinite(x).all() and np.isfinite(y).all()):
+        raise AssertionError("native linear contains nonfinite operands or outputs")
+    steps = k + 12
+    gamma32 = steps * 2.0**-24 / (1.0 - steps * 2.0**-24)
+    gamma64 = k * 2.0**-53 / (1.0 - k * 2.0**-53)
+    uout = 2.0**-7 / 2.0          # torch.finfo(bfloat16).eps / 2
+    underflow = 2.0**-126 * uout  # torch.finfo(bfloat16).tiny * uout
+    anchor = x @ w.T
+    bound = (np.abs(x) @ np.abs(w).T) * ((gamma32 + gamma64) / (1.0 - gamma64)) * (1.0 + uout)
+    bound += np.abs(anchor) * uout + underflow
+    error = np.abs(y - anchor)
+    if not np.isfinite(error).all() or (error > bound).any():
+        raise AssertionError(
+            f"native linear exceeds FP32/format/RNE enclosure: excess={(error - bound).max()}")
+    return dict(rows=x.shape[0], outputs=w.shape[0], reduction_length=k,
+                max_abs_error=float(error.max()), max_bound=float(bound.max()))
+
+
+# --------------------------------------------------------------------------- #
+# A13-A15: acceptance
+# --------------------------------------------------------------------------- #
+def candidates(logits_bits: np.ndarray, temperatures: np.ndarray, count: int, capacity: int | None = None,
+               owned_rows: int | None = None, all_random: bool = False):
+    """[M, V] bf16 logits -> ([M, capacity] bf16 scores, [M, capacity] int64 ids)."""
+    logits_bits = _c(logits_bits, np.uint16)
+    rows, width = logits_bits.shape
+    capacity = count if capacity is None else capacity
+    owned_rows = rows if owned_rows is None else owned_rows
+    temps = _c(temperatures, np.float32)
+    scores = np.empty((rows, capacity), np.uint16)
+    ids = np.empty((rows, capacity), np.int64)
+    rc = lib().oracle_candidates(_p(logits_bits), ctypes.c_int64(rows), ctypes.c_int64(width),
+                                 ctypes.c_int64(width), _p(temps), ctypes.c_int64(owned_rows),
+                                 ctypes.c_int(count), ctypes.c_int(capacity), ctypes.c_int(int(all_random)),
+                                 _p(scores), _p(ids))
+    if rc:
+        raise ValueError("invalid candidate count")
+    return scores, ids
+
+
+def verify_k1(q_scores, q_ids, p_scores, p_ids, target_rows, draft_tokens, temperatures, top_ps,
+              top_ks, seeds, ordinals, active_rows: int, uniforms=None, allow_underfilled=False,
+              constrained_rows=None) -> np.ndarray:
+    """Decisions [C, 2] int64 for bf16-bit candidate arrays [TP, rows, K]."""
+    q_scores, p_scores = _c(q_scores, np.uint16), _c(p_scores, np.uint16)
+    q_ids, p_ids = _c(q_ids, np.int64), _c(p_ids, np.int64)
+    tp, q_rows, k = q_scores.shape
+    p_rows = p_scores.shape[1]
+    dec = np.empty((q_rows, 2), np.int64)
+    uni = None if uniforms is None else _c(uniforms, np.float32)
+    con = None if constrained_rows is None else _c(constrained_rows, np.uint8)
+    rc = lib().oracle_verify_k1(
+        _p(q_scores), _p(q_ids), _p(p_scores), _p(p_ids), _p(_c(target_rows, np.int32)),
+        _p(_c(draft_tokens, np.int64)), _p(_c(temperatures, np.float32)), _p(_c(top_ps, np.float32)),
+        _p(_c(top_ks, np.int64)), _p(_c(seeds, np.int64)), _p(_c(ordinals, np.int64)), _p(uni),
+        _p(con), ctypes.c_int(int(allow_underfilled)), ctypes.c_int(tp), ctypes.c_int(q_rows),
+        ctypes.c_int(p_rows), ctypes.c_int(k), ctypes.c_int(active_rows), _p(dec))
+    if rc:
+        raise ValueError("candidate block too wide")
+    return dec
+
+
+def merge_prefix(decisions: np.ndarray, live_rows: int) -> np.ndarray:
+    decisions = _c(decisions, np.int64)
+    depth, c, _ = decisions.shape
+    out = np.empty((c, 2), np.int64)
+    lib().oracle_merge_prefix(_p(decisions), ctypes.c_int(c), ctypes.c_int(depth),
+                              ctypes.c_int(live_rows), _p(out))
+    return out
+
+
+def verify_from_logits(logits_bits, q_scores, q_ids, draft_tokens, temperatures, top_ps, top_ks,
+                       seeds, ordinals, live_rows: int, uniforms=None, count: int = 20):
+    """Composition A13 -> A14 (per depth) -> A15 for C sequences of depth D.
+
+    logits: [C*(D+1), V] bf16 bits, row c*(D+1)+d.  q_*: [D, C, K].  Per-depth
+    parameters: [D, C].  Target-row temperatures repeat each sequence's depth-0
+    temperature (executor/draft_graph.py:1049-1054).  Returns (candidate scores,
+    candidate ids, per-depth decisions [D, C, 2], merged [C, 2]).
+    """
+    depth, c, k = np.asarray(q_ids).shape
+    temps = _c(temperatures, np.float32)
+    row_t = np.repeat(temps[0], depth + 1)
+    p_scores, p_ids = candidates(logits_bits, row_t, count, owned_rows=live_rows * (depth + 1))
+    rows = np.arange(c, dtype=np.int32) * (depth + 1)
+    dec = np.empty((depth, c, 2), np.int64)
+    for d in range(depth):
+        dec[d] = verify_k1(np.asarray(q_scores)[d][None], np.asarray(q_ids)[d][None], p_scores[None],
+                           p_ids[None], rows + d, np.asarray(draft_tokens)[d], temps[d],
+                           np.asarray(top_ps)[d], np.asarray(top_ks)[d], np.asarray(seeds)[d],
+                           np.asarray(ordinals)[d], live_rows,
+                           None if uniforms is None else np.asarray(uniforms)[d])
+    return p_scores, p_ids, dec, merge_prefix(dec, live_rows)
+
+
+if os.environ.get("CUBIC_ORACLE_BUILD_ON_IMPORT") == "1":  # pragma: no cover
+    build()
