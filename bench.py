@@ -1,0 +1,281 @@
+"""MTP verify-step benchmark on one MI355X.
+
+One step = the Cubic linears of the Qwen3-8B-shaped target forward at M = 64
+(batch 32 x (k=1 draft + 1 bonus)): for each of ``--layers`` layers qkv
+(4096 -> 6144), o (4096 -> 4096), gate/up (4096 -> 2 x 12288, one grouped
+launch) and down (12288 -> 4096); then the W4 lm_head (4096 -> 151936); then
+the fused greedy acceptance over the [64, 151936] logits.  Weights are Cubic
+4-bit, group 128, encoded from N(0, 0.02); activations bf16 N(0, 1); draft
+tokens match the target argmax for ~70% of sequences.  Every layer streams its
+own copy of the prepared weights (distinct HBM), so nothing is served from the
+256 MB last-level cache across layers.  The step is captured once in a HIP
+graph and replayed; inputs are resident in HBM before the timed region.
+
+Prints one JSON line: value = algorithmic bytes of the step / step time
+(GB/s); roofline for the dominant kernel (the lm_head GEMM); cpu_baseline =
+the CPU oracle on a bounded sample of the same step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+M_ROWS, HIDDEN, VOCAB = 64, 4096, 151936
+QKV, INTER = 6144, 12288
+BITS, GROUP = 4, 128
+C_SEQ, DEPTH = 32, 1
+
+
+def gemm_bytes(m: int, n: int, k: int, bits: int = BITS, group: int = GROUP) -> int:
+    """Algorithmic bytes: codes + fmt0 metadata (8 B/group) + x + y."""
+    return n * k * bits // 8 + n * (-(-k // group)) * 8 + m * k * 2 + m * n * 2
+
+
+def step_bytes(layers: int) -> dict:
+    per_layer = (gemm_bytes(M_ROWS, QKV, HIDDEN) + gemm_bytes(M_ROWS, HIDDEN, HIDDEN)
+                 + gemm_bytes(M_ROWS, 2 * INTER, HIDDEN) + gemm_bytes(M_ROWS, HIDDEN, INTER))
+    lm_head = gemm_bytes(M_ROWS, VOCAB, HIDDEN)
+    accept = M_ROWS * VOCAB * 2
+    return {"per_layer": per_layer, "lm_head": lm_head, "accept": accept,
+            "total": layers * per_layer + lm_head + accept}
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=6144,
+                    help="lm_head rows in the CPU-baseline sample")
+    ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                      "profiles", "gemm_lm_head_cfg2_traffic.json"))
+    return ap.parse_args(argv)
+
+
+def build_step(layers: int):
+    import torch
+
+    from cubic_serve_amd import linear, quantization as qz, sampling
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def encode(n, k):
+        w = torch.randn((n, k), generator=gen, device=dev) * 0.02
+        m = qz.quantize_cubic(w, bits=BITS, group_in=GROUP)
+        del w
+        return linear.prepare_matrix(m, dev)
+
+    proto = {"qkv": encode(QKV, HIDDEN), "o": encode(HIDDEN, HIDDEN),
+             "gate": encode(INTER, HIDDEN), "up": encode(INTER, HIDDEN), "down": encode(HIDDEN, INTER)}
+    lm_head = encode(VOCAB, HIDDEN)
+    xg = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn((M_ROWS, HIDDEN), generator=xg, device=dev).to(torch.bfloat16)
+    x_down = torch.randn((M_ROWS, INTER), generator=xg, device=dev).to(torch.bfloat16)
+    y_qkv = torch.empty((M_ROWS, QKV), dtype=torch.bfloat16, device=dev)
+    y_o = torch.empty((M_ROWS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    y_gate = torch.empty((M_ROWS, INTER), dtype=torch.bfloat16, device=dev)
+    y_up = torch.empty((M_ROWS, INTER), dtype=torch.bfloat16, device=dev)
+    y_down = torch.empty((M_ROWS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((M_ROWS, VOCAB), dtype=torch.bfloat16, device=dev)
+
+    layer_bindings = []
+    gate_up = None
+    for layer in range(layers):
+        w = {k: (v if layer == 0 else linear.clone_prepared(v)) for k, v in proto.items()}
+        gate_up = linear.PreparedCubic(torch.cat([w["gate"].codes, w["up"].codes]),
+                                       torch.cat([w["gate"].meta, w["up"].meta]), 2 * INTER, HIDDEN,
+                                       BITS, GROUP)
+        layer_bindings += [
+            linear.bind_prepared(x, w["qkv"], (y_qkv,)),
+            linear.bind_prepared(x, w["o"], (y_o,)),
+            linear.bind_prepared(x, gate_up, (y_gate, y_up), (INTER, INTER)),
+            linear.bind_prepared(x_down, w["down"], (y_down,)),
+        ]
+        del w
+    del proto
+    lm_binding = linear.bind_prepared(x, lm_head, (logits,))
+    lm_binding.launch()
+    torch.cuda.synchronize()
+
+    # drafts: ~70% equal the argmax of their target row
+    rows = torch.arange(C_SEQ, device=dev) * (DEPTH + 1)
+    top = logits.float().argmax(-1)[rows]
+    dg = torch.Generator(device=dev).manual_seed(2)
+    hit = torch.rand(C_SEQ, generator=dg, device=dev) < 0.7
+    other = (top + 1 + torch.randint(0, VOCAB - 1, (C_SEQ,), generator=dg, device=dev)) % VOCAB
+    drafts = torch.where(hit, top, other).reshape(DEPTH, C_SEQ).contiguous()
+    q_scores = torch.full((DEPTH, C_SEQ, 20), float("nan"), dtype=torch.bfloat16, device=dev)
+    q_scores[:, :, 0] = 1.0
+    q_ids = torch.full((DEPTH, C_SEQ, 20), -1, dtype=torch.int64, device=dev)
+    q_ids[:, :, 0] = drafts
+    zeros_f = torch.zeros((DEPTH, C_SEQ), dtype=torch.float32, device=dev)
+    plan = sampling.MTPVerifyPlan(
+        logits=logits, q_scores=q_scores, q_token_ids=q_ids, draft_tokens=drafts,
+        temperatures=zeros_f, top_ps=torch.ones_like(zeros_f),
+        top_ks=torch.full((DEPTH, C_SEQ), 20, dtype=torch.int64, device=dev),
+        seeds=torch.zeros((DEPTH, C_SEQ), dtype=torch.int64, device=dev),
+        ordinals=torch.zeros((DEPTH, C_SEQ), dtype=torch.int64, device=dev))
+    return dict(layer_bindings=layer_bindings, lm_binding=lm_binding, plan=plan, logits=logits,
+                x=x, lm_head=lm_head, drafts=drafts, hit=hit)
+
+
+def capture(fn):
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # eager warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, reps: int, warmup: int) -> float:
+    """Average ms per replay, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(step: dict, rows: int) -> dict:
+    """CPU oracle (scalar C, 1 thread) on a bounded sample of the same step:
+    decode + bf16 round + FP32 dot for lm_head rows [0, rows) at M = 64, and
+    the candidate preparation of all 64 logit rows."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle
+    from cubic_serve_amd import quantization as qz
+
+    oracle.build()
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn((rows, HIDDEN), generator=g) * 0.02
+    m = qz.quantize_cubic(w, bits=BITS, group_in=GROUP)
+    payload = {k: v.numpy() for k, v in m.payload.items()}
+    x = step["x"].cpu().view(torch.int16).numpy().view(np.uint16)
+    logits = step["logits"].cpu().view(torch.int16).numpy().view(np.uint16)
+    t0 = time.perf_counter()
+    wb = oracle.decode_bf16(payload, BITS, qz.FMT_F32, (rows, HIDDEN), GROUP)
+    oracle.linear_bf16(x, wb)
+    t1 = time.perf_counter()
+    oracle.candidates(logits, np.zeros(M_ROWS, np.float32), 20)
+    t2 = time.perf_counter()
+    nbytes = gemm_bytes(M_ROWS, rows, HIDDEN) + M_ROWS * VOCAB * 2
+    return {"value": round(nbytes / (t2 - t0) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/cubic_oracle.c: lm_head rows [0,{rows}) x K=4096 W4 at M=64 "
+                      f"(decode, bf16 round, FP32 dot: {t1 - t0:.2f}s) + candidates over "
+                      f"[64,151936] logits ({t2 - t1:.2f}s); same algorithmic-byte accounting"}
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    step = build_step(args.layers)
+
+    def run_step():
+        for b in step["layer_bindings"]:
+            b.launch()
+        step["lm_binding"].launch()
+        step["plan"].launch()
+
+    graph = capture(run_step)
+    # correctness guard on the timed path: the fused acceptance accepted the
+    # planted drafts (~70%) of the greedy step
+    graph.replay()
+    torch.cuda.synchronize()
+    accepted = int((step["plan"].merged[:, 0] == 1).sum())
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    # component breakdown and the dominant kernel's launch duration
+    lm_graph = capture(lambda: step["lm_binding"].launch())
+    lm_ms = time_graph(lm_graph, 50, 5)
+    acc_graph = capture(lambda: step["plan"].launch())
+    acc_ms = time_graph(acc_graph, 200, 10)
+
+    nb = step_bytes(args.layers)
+    value = nb["total"] / (ms_per_step * 1e-3) / 1e9
+    lm_gbs = nb["lm_head"] / (lm_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    result = {
+        "metric": "verify-step µs + Cubic-GEMM HBM GB/s (% peak), Qwen3-8B-shaped W4, M=64",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"cfg2 verify step: {args.layers} Qwen3-8B-shaped layers (qkv, o, "
+                               "gate/up, down) + lm_head 4096x151936, Cubic W4 g128, M=64 "
+                               "(batch 32, k=1), fused greedy acceptance",
+                   "m": M_ROWS, "layers": args.layers, "bits": BITS, "group": GROUP},
+        "verify_step_us": round(ms_per_step * 1e3, 2),
+        "step_hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "lm_head_us": round(lm_ms * 1e3, 2),
+        "accept_us": round(acc_ms * 1e3, 2),
+        "accept_gbs": round(nb["accept"] / (acc_ms * 1e-3) / 1e9, 2),
+        "layers_us": round((ms_per_step - lm_ms - acc_ms) * 1e3, 2),
+        "greedy_accepted": f"{accepted}/{C_SEQ}",
+        "wall_s": round(wall, 3),
+        "roofline": {"kernel": "gemm_kernel<4,4,4> (lm_head)", "bound": "hbm",
+                     "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": nb["lm_head"]},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(step, args.cpu_rows)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,77 @@
+"""Build the gfx950 HIP library in-tree: cubic_serve_amd/_lib/libcubic_mi355x.so.
+
+hipcc cross-compiles on a machine without a GPU.  Flags:
+  -ffp-contract=off   the Cubic decoder and acceptance transform are unfused IEEE
+  -Xclang -target-feature -Xclang -packed-fp32-ops   no packed FP32 instructions
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = PACKAGE / "csrc"
+LIB_DIR = PACKAGE / "_lib"
+LIB = LIB_DIR / "libcubic_mi355x.so"
+SOURCES = ("cubic_capi.hip", "cubic_gemm.hip", "cubic_accept.hip")
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the Cubic MI355X library needs ROCm's hipcc")
+
+
+def flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
+        f"-I{ROOT / 'include'}", f"-I{CSRC}",
+    ]
+
+
+def build(verbose: bool = False, jobs: int = 3) -> Path:
+    """Compile every HIP source (in parallel) and link the shared library."""
+    LIB_DIR.mkdir(exist_ok=True)
+    obj_dir = LIB_DIR / "obj"
+    obj_dir.mkdir(exist_ok=True)
+    cc = hipcc()
+    procs = []
+    objects = []
+    for src in SOURCES:
+        obj = obj_dir / (Path(src).stem + ".o")
+        objects.append(obj)
+        cmd = [cc, *flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+        while sum(p.poll() is None for _, p in procs) >= jobs:
+            procs[[p.poll() is None for _, p in procs].index(True)][1].wait()
+    failed = []
+    for src, p in procs:
+        out = p.communicate()[0].decode(errors="replace")
+        lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+        if p.returncode != 0:
+            failed.append((src, "\n".join(lines)))
+        elif verbose and lines:
+            print("\n".join(lines))
+    if failed:
+        raise RuntimeError("HIP build failed:\n" + "\n\n".join(f"[{s}]\n{o}" for s, o in failed))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError("HIP link failed:\n" + res.stdout.decode(errors="replace"))
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,801 @@
+// MTP acceptance on gfx950: candidate selection over the vocabulary, p/q
+// verification of each draft depth, and the accepted-prefix merge.
+//
+// Reference semantics (paths under src/cubic_serve/ of QuantTrio/cubic-serve):
+//   candidates   ops/cuda/sampling/local_candidates.py:206-226,
+//                local_candidates.cu:19-146, greedy.cu:14-78
+//   verify       ops/cuda/sampling/speculative.py:46-219
+//   merge        executor/draft_graph.py:146-157
+//
+// One HBM pass over the logits: each workgroup owns a (row, vocab tile) and
+// reduces it to its 20 best (value desc, id asc) entries plus a finiteness
+// flag; the last workgroup to finish a group of rows (one row for plain
+// candidate preparation, the k+1 rows of one sequence for the fused verify)
+// merges the tiles, publishes the candidates and, in fused mode, verifies
+// every depth and merges the prefix.  Arrival counters live in the caller's
+// workspace; the finishing workgroup returns its counter to zero.
+//
+// Wave-level reductions follow fixed orders (butterfly sums, Kogge-Stone
+// scans) that the CPU restatement reproduces operation for operation.
+#include "cubic_device.h"
+#include "cubic_capi_internal.h"
+
+namespace cubic {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTop = 20;              // tile candidates kept per (row, tile)
+constexpr int kMaxTileChunks = 16;    // 16 x 2048 = 32768 elements per tile
+constexpr int kMaxTiles = 24;         // tiles per row (final merge holds 8 entries per lane)
+constexpr int kChunk = kThreads * 8;  // elements per 16-byte load round
+constexpr int64_t kInt64Max = 0x7FFFFFFFFFFFFFFFLL;
+
+// --------------------------------------------------------------------------
+// Ordering keys.  key16 maps bf16 bits to an unsigned order that compares like
+// the float values and treats -0 and +0 as equal; the low 16 bits hold
+// 0xFFFF - local index so that the larger composite is the lower id on ties.
+// --------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t order_key16(uint32_t u) {
+    const uint32_t m = u & 0x7FFFu;
+    return (u & 0x8000u) ? 0x8000u - m : 0x8000u + m;
+}
+
+__device__ __forceinline__ uint32_t key16_to_bf16(uint32_t k) {
+    return k >= 0x8000u ? k - 0x8000u : (0x8000u | (0x8000u - k));
+}
+
+__device__ __forceinline__ bool nonfinite_bf16(uint32_t u) { return (u & 0x7F80u) == 0x7F80u; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint32_t o = __shfl_xor(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Descending bitonic sort of one u32 per lane across the wave.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane) {
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+            const uint32_t o = __shfl_xor(v, stride);
+            const bool upper = (lane & stride) != 0;
+            const bool desc = (lane & size) == 0;
+            const uint32_t hi = o > v ? o : v, lo = o > v ? v : o;
+            v = (upper == desc) ? lo : hi;
+        }
+    }
+    return v;
+}
+
+// --------------------------------------------------------------------------
+// Verification of one proposal row by one wave (speculative.py:46-219).
+// Virtual lanes v = lane + 64 * s, s < SLOTS, cover BLOCK = next_pow2(TP*K).
+// --------------------------------------------------------------------------
+struct VerifyRow {
+    const uint16_t* q_scores;  // rank 0 entry of this row; rank r at + r * q_rank_stride
+    const int64_t* q_ids;
+    const uint16_t* p0_scores;
+    const int64_t* p0_ids;
+    const uint16_t* p1_scores;
+    const int64_t* p1_ids;
+    int64_t q_rank_stride, p_rank_stride;
+    int tp, k, block;
+    bool active, rows_ok;
+    int64_t draft;
+    float temperature, top_p;
+    int64_t top_k, seed, ordinal;
+    const float* uniforms;  // two floats or null
+    bool underfilled;
+};
+
+template <int SLOTS>
+struct VerifyScratch {
+    float score[3][SLOTS * kWave];
+    int64_t id[3][SLOTS * kWave];
+    int real[3][SLOTS * kWave];
+    float sorted_score[3][SLOTS * kWave];
+    int64_t sorted_id[3][SLOTS * kWave];
+    float qprob[SLOTS * kWave];
+};
+
+template <int SLOTS>
+__device__ __forceinline__ float vl_tree_sum(float (&x)[SLOTS], int block) {
+    // butterfly x[i] += x[i ^ m], m = block/2 .. 1
+    for (int m = block >> 1; m >= 1; m >>= 1) {
+        if (m >= kWave) {
+            const int sm = m / kWave;
+            float y[SLOTS];
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) y[s] = x[s] + x[s ^ sm];
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
+        } else {
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) x[s] = x[s] + __shfl_xor(x[s], m);
+        }
+    }
+    return __shfl(x[0], 0);
+}
+
+template <int SLOTS>
+__device__ __forceinline__ void vl_scan(float (&x)[SLOTS], int block, int lane) {
+    // Kogge-Stone inclusive scan x[i] += x[i - d], d = 1 .. block/2
+    for (int d = 1; d < block; d <<= 1) {
+        float y[SLOTS];
+        if (d >= kWave) {
+            const int sd = d / kWave;
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) y[s] = s >= sd ? x[s] + x[s - sd] : x[s];
+        } else {
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) {
+                const float same = __shfl(x[s], lane - d);              // lane >= d
+                const float prev = __shfl(x[s > 0 ? s - 1 : 0], lane + kWave - d);  // lane < d
+                const int v = lane + kWave * s;
+                const float other = lane >= d ? same : prev;
+                y[s] = v >= d ? x[s] + other : x[s];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
+    }
+}
+
+template <int SLOTS>
+__device__ __forceinline__ float vl_max(const float (&x)[SLOTS], int block) {
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) m = x[s] > m ? x[s] : m;  // NaN-ignoring
+    for (int w = (block < kWave ? block : kWave) >> 1; w >= 1; w >>= 1) {
+        const float o = __shfl_xor(m, w);
+        m = o > m ? o : m;
+    }
+    return __shfl(m, 0);
+}
+
+// speculative.py:11-29 on the LDS copy of one candidate set.  Writes the
+// selected (score, id) pairs in rank order to sorted_*, returns the number of
+// real lanes.  A real lane is the first of its (score, id) pair if no earlier
+// real lane repeats it; its rank is the number of first lanes strictly ahead
+// in (score desc, id asc) order.  Duplicated pairs therefore occupy one slot,
+// exactly as the reference removes every copy when it selects the pair.
+template <int SLOTS>
+__device__ int select_topk(VerifyScratch<SLOTS>& sc, int set, int block, int k, int lane) {
+    const float* score = sc.score[set];
+    const int64_t* id = sc.id[set];
+    int* real = sc.real[set];  // 0 = not real, 1 = real repeat, 2 = real first
+    float my_s[SLOTS];
+    int64_t my_i[SLOTS];
+    bool my_r[SLOTS], first[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        my_r[s] = v < block && real[v];
+        my_s[s] = v < block ? score[v] : 0.0f;
+        my_i[s] = v < block ? id[v] : 0;
+        first[s] = my_r[s];
+    }
+    int count = 0;
+    for (int j = 0; j < block; ++j) {
+        const bool rj = real[j] != 0;
+        count += rj;
+        if (!rj) continue;
+        const float sj = score[j];
+        const int64_t ij = id[j];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s)
+            if (my_r[s] && j < lane + kWave * s && sj == my_s[s] && ij == my_i[s]) first[s] = false;
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        if (v < block) {
+            real[v] = my_r[s] ? (first[s] ? 2 : 1) : 0;
+            sc.sorted_score[set][v] = -__builtin_huge_valf();
+            sc.sorted_id[set][v] = kInt64Max;
+        }
+    }
+    wave_lds_sync();
+    int rank[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) rank[s] = 0;
+    for (int j = 0; j < block; ++j) {
+        if (real[j] != 2) continue;
+        const float sj = score[j];
+        const int64_t ij = id[j];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s)
+            rank[s] += (sj > my_s[s] || (sj == my_s[s] && ij < my_i[s])) ? 1 : 0;
+    }
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+        if (my_r[s] && first[s] && rank[s] < k) {
+            sc.sorted_score[set][rank[s]] = my_s[s];
+            sc.sorted_id[set][rank[s]] = my_i[s];
+        }
+    wave_lds_sync();
+    return count;
+}
+
+// speculative.py:32-43 for the sorted scores of one set.
+template <int SLOTS>
+__device__ __forceinline__ void probabilities(const float* sorted, float temperature, int64_t top_k,
+                                              float top_p, int block, int lane, float (&out)[SLOTS],
+                                              float& mass) {
+    const float safe_t = temperature == 0.0f ? 1.0f : temperature;
+    float logit[SLOTS], w[SLOTS], p[SLOTS], incl[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        const bool sel = v < block && v < top_k;
+        logit[s] = sel ? sorted[v] / safe_t : -__builtin_huge_valf();
+    }
+    const float mx = vl_max<SLOTS>(logit, block);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        const bool sel = v < block && v < top_k;
+        w[s] = sel ? accept_expf(logit[s] - mx) : 0.0f;
+    }
+    float tmp[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) tmp[s] = w[s];
+    const float sum = vl_tree_sum<SLOTS>(tmp, block);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) { p[s] = w[s] / sum; incl[s] = p[s]; }
+    vl_scan<SLOTS>(incl, block, lane);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        const float excl = incl[s] - p[s];
+        p[s] = (v < block && v < top_k && excl <= top_p) ? p[s] : 0.0f;
+        tmp[s] = p[s];
+    }
+    mass = vl_tree_sum<SLOTS>(tmp, block);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) out[s] = p[s] / mass;
+}
+
+template <int SLOTS>
+__device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int lane, int64_t* out2) {
+    const int block = r.block;
+    bool lane_ok = true;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        if (v >= block) continue;
+        const bool cm = v < r.tp * r.k;
+        const int rank = cm ? v / r.k : 0, local = cm ? v % r.k : 0;
+        const bool load = r.active && cm;
+        const bool load_p = load && r.rows_ok;
+        float qs = -__builtin_huge_valf(), p0s = qs, p1s = qs;
+        int64_t qi = -1, p0i = -1, p1i = -1;
+        if (load) {
+            qs = bf16_bits_to_float(r.q_scores[rank * r.q_rank_stride + local]);
+            qi = r.q_ids[rank * r.q_rank_stride + local];
+        }
+        if (load_p) {
+            p0s = bf16_bits_to_float(r.p0_scores[rank * r.p_rank_stride + local]);
+            p0i = r.p0_ids[rank * r.p_rank_stride + local];
+            p1s = bf16_bits_to_float(r.p1_scores[rank * r.p_rank_stride + local]);
+            p1i = r.p1_ids[rank * r.p_rank_stride + local];
+        }
+        const bool qr = cm && qi >= 0 && __builtin_fabsf(qs) < __builtin_huge_valf();
+        const bool p0r = cm && p0i >= 0 && __builtin_fabsf(p0s) < __builtin_huge_valf();
+        const bool p1r = cm && p1i >= 0 && __builtin_fabsf(p1s) < __builtin_huge_valf();
+        const bool qpad = cm && qi == -1 && qs != qs;
+        const bool p0pad = cm && p0i == -1 && p0s != p0s;
+        const bool p1pad = cm && p1i == -1 && p1s != p1s;
+        lane_ok = lane_ok && (!cm || qr || qpad) && (!cm || p0r || p0pad) && (!cm || p1r || p1pad);
+        sc.score[0][v] = qs; sc.id[0][v] = qi; sc.real[0][v] = qr;
+        sc.score[1][v] = p0s; sc.id[1][v] = p0i; sc.real[1][v] = p0r;
+        sc.score[2][v] = p1s; sc.id[2][v] = p1i; sc.real[2][v] = p1r;
+    }
+    const bool pairs_valid = __all(lane_ok);
+    wave_lds_sync();
+    const int qc = select_topk<SLOTS>(sc, 0, block, r.k, lane);
+    const int p0c = select_topk<SLOTS>(sc, 1, block, r.k, lane);
+    const int p1c = select_topk<SLOTS>(sc, 2, block, r.k, lane);
+
+    float qp[SLOTS], p0p[SLOTS], p1p[SLOTS], qm, p0m, p1m;
+    probabilities<SLOTS>(sc.sorted_score[0], r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
+    probabilities<SLOTS>(sc.sorted_score[1], r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
+    probabilities<SLOTS>(sc.sorted_score[2], r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
+
+    int64_t iq[SLOTS], ip0[SLOTS], ip1[SLOTS];
+    float t1[SLOTS], t2[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        iq[s] = v < block ? sc.sorted_id[0][v] : kInt64Max;
+        ip0[s] = v < block ? sc.sorted_id[1][v] : kInt64Max;
+        ip1[s] = v < block ? sc.sorted_id[2][v] : kInt64Max;
+        t1[s] = iq[s] == r.draft ? qp[s] : 0.0f;
+        t2[s] = ip0[s] == r.draft ? p0p[s] : 0.0f;
+        if (v < block) sc.qprob[v] = qp[s];
+    }
+    const float q_draft = vl_tree_sum<SLOTS>(t1, block);
+    const float p_draft = vl_tree_sum<SLOTS>(t2, block);
+    const float quotient = p_draft / q_draft;
+    const float ratio = quotient < 1.0f ? quotient : 1.0f;
+    const uint32_t key = (uint32_t)(r.seed ^ (r.seed >> 32) ^ 0x9E3779B9LL);
+    const float u_accept = r.uniforms ? r.uniforms[0] : philox_uniform(key, (uint32_t)(r.ordinal * 2));
+    const bool random_accepted = u_accept < ratio;
+    const bool greedy = r.temperature == 0.0f;
+    const int64_t p0_top = __shfl(ip0[0], 0), p1_top = __shfl(ip1[0], 0);
+    const bool greedy_accepted = r.draft == p0_top;
+    const bool accepted = greedy ? greedy_accepted : random_accepted;
+    wave_lds_sync();
+
+    float q_at_p[SLOTS], residual[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) q_at_p[s] = 0.0f;
+    for (int pos = 0; pos < r.k; ++pos) {
+        const int64_t qid = sc.sorted_id[0][pos];
+        const float qpr = sc.qprob[pos];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) q_at_p[s] = ip0[s] == qid ? qpr : q_at_p[s];
+    }
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const float d = p0p[s] - q_at_p[s];
+        residual[s] = d > 0.0f ? d : 0.0f;
+        t1[s] = residual[s];
+    }
+    const float rmass = vl_tree_sum<SLOTS>(t1, block);
+    const float u_sample = r.uniforms ? r.uniforms[1]
+                                      : philox_uniform(key ^ 0x85EBCA6Bu, (uint32_t)(r.ordinal * 2 + 1));
+    float c1[SLOTS], cr[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) { c1[s] = p1p[s]; cr[s] = residual[s]; }
+    vl_scan<SLOTS>(c1, block, lane);
+    vl_scan<SLOTS>(cr, block, lane);
+    const float scaled_u = u_sample * rmass;
+    int p1_slot = block, res_slot = block;
+#pragma unroll
+    for (int s = SLOTS - 1; s >= 0; --s) {
+        const int v = lane + kWave * s;
+        const uint64_t b1 = __ballot(v < block && c1[s] > u_sample);
+        const uint64_t br = __ballot(v < block && cr[s] > scaled_u);
+        if (b1) p1_slot = kWave * s + __builtin_ctzll(b1);
+        if (br) res_slot = kWave * s + __builtin_ctzll(br);
+    }
+    const int64_t p1_token = p1_slot < block ? sc.sorted_id[2][p1_slot] : kInt64Max;
+    const int64_t res_token = res_slot < block ? sc.sorted_id[1][res_slot] : kInt64Max;
+    const int64_t need = (greedy || r.underfilled) ? 1 : r.top_k;
+    const bool valid = r.active && pairs_valid && r.rows_ok && r.temperature >= 0.0f &&
+                       r.temperature < __builtin_huge_valf() && r.top_k >= 1 && r.top_k <= r.k &&
+                       r.top_p > 0.0f && r.top_p <= 1.0f && r.seed >= 0 && r.ordinal >= 0 &&
+                       qc >= need && p0c >= need && p1c >= need && qm > 0.0f && p0m > 0.0f &&
+                       p1m > 0.0f && q_draft > 0.0f && (greedy || accepted || rmass > 0.0f);
+    const int64_t greedy_next = greedy_accepted ? p1_top : p0_top;
+    const int64_t next = greedy ? greedy_next : (accepted ? p1_token : res_token);
+    if (lane == 0) {
+        out2[0] = valid ? (int64_t)accepted : -1;
+        out2[1] = valid ? next : -1;
+    }
+    wave_lds_sync();
+}
+
+// --------------------------------------------------------------------------
+// Standalone verify: one wave per proposal row.
+// --------------------------------------------------------------------------
+template <int SLOTS>
+__global__ __launch_bounds__(kWave) void verify_candidates_kernel(VerifyArgs a) {
+    __shared__ VerifyScratch<SLOTS> sc;
+    const int row = blockIdx.x, lane = threadIdx.x;
+    VerifyRow r;
+    r.active = row < a.active_rows;
+    const int32_t target = r.active ? a.target_rows[row] : 0;
+    r.rows_ok = target >= 0 && target + 1 < a.p_rows;
+    const int64_t t = r.rows_ok ? target : 0;
+    r.q_scores = a.q_scores + (int64_t)row * a.k;
+    r.q_ids = a.q_ids + (int64_t)row * a.k;
+    r.p0_scores = a.p_scores + t * a.k;
+    r.p0_ids = a.p_ids + t * a.k;
+    r.p1_scores = r.p0_scores + a.k;
+    r.p1_ids = r.p0_ids + a.k;
+    r.q_rank_stride = (int64_t)a.q_rows * a.k;
+    r.p_rank_stride = (int64_t)a.p_rows * a.k;
+    r.tp = a.tp;
+    r.k = a.k;
+    r.block = a.block;
+    r.draft = r.active ? a.draft_tokens[row] : -1;
+    r.temperature = r.active ? a.temperatures[row] : 1.0f;
+    r.top_p = r.active ? a.top_ps[row] : 1.0f;
+    r.top_k = r.active ? a.top_ks[row] : 1;
+    r.seed = r.active ? a.seeds[row] : 0;
+    r.ordinal = r.active ? a.ordinals[row] : 0;
+    r.uniforms = a.uniforms ? a.uniforms + 2 * (int64_t)row : nullptr;
+    bool under = a.allow_underfilled != 0;
+    if (a.constrained_rows) under = under && r.active && a.constrained_rows[row];
+    r.underfilled = under;
+    verify_wave<SLOTS>(r, sc, lane, a.decisions + 2 * (int64_t)row);
+}
+
+// merge_prefix: decisions [depth, c, 2] -> out [c, 2]
+__global__ __launch_bounds__(kThreads) void merge_prefix_kernel(const int64_t* decisions, int c,
+                                                                 int depth, const int32_t* live,
+                                                                 int live_rows, int64_t* out) {
+    const int live_count = live ? live[0] : live_rows;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < c; r += gridDim.x * blockDim.x) {
+        int64_t accepted = depth, bonus = decisions[((int64_t)(depth - 1) * c + r) * 2 + 1];
+        bool good = true;
+        for (int d = depth - 1; d >= 0; --d) {
+            const int64_t av = decisions[((int64_t)d * c + r) * 2];
+            const int64_t tok = decisions[((int64_t)d * c + r) * 2 + 1];
+            if (av == 0) { accepted = d; bonus = tok; }
+            good = good && (av == 0 || av == 1) && tok >= 0;
+        }
+        const bool ok = r < live_count && good;
+        out[2 * (int64_t)r] = ok ? accepted : -1;
+        out[2 * (int64_t)r + 1] = ok ? bonus : -1;
+    }
+}
+
+// --------------------------------------------------------------------------
+// Candidate tiles + group finalisation (plain candidates or fused verify).
+// --------------------------------------------------------------------------
+struct TileScratch {
+    uint32_t survivors[kWaves][kWave];
+    uint32_t wave_top[kWaves * kTop];
+    uint32_t flags[kWaves];
+    uint32_t last;
+    // finalisation: candidates of the group rows (count <= 64, rows <= 9)
+    uint16_t cand_score[9][64];
+    int64_t cand_id[9][64];
+    int64_t decisions[8][2];
+};
+
+// Exact top-`kTop` composites of the lane-held elements of one wave.
+// keys are recomputed from the raw bf16 words (E chunks of 8 per lane).
+template <int EMAX>
+__device__ __forceinline__ uint32_t elem_composite(const uint4 (&raw)[EMAX], int e, int j,
+                                                   uint32_t base_idx, int width_left) {
+    const uint32_t word = (&raw[e].x)[j >> 1];
+    const uint32_t u = (j & 1) ? (word >> 16) : (word & 0xFFFFu);
+    const int idx = (int)base_idx + e * kChunk + j;
+    if (idx >= width_left) return 0u;
+    return (order_key16(u) << 16) | (0xFFFFu - (uint32_t)idx);
+}
+
+template <int EMAX>
+__device__ void tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
+                         TileScratch& ts, int lane, int wave, uint32_t* out_top) {
+    // 1. lane maxima
+    uint32_t lane_max = 0;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+        if (e >= chunks) break;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
+            lane_max = c > lane_max ? c : lane_max;
+        }
+    }
+    // 2. threshold: the kTop-th largest lane maximum bounds the kTop-th element
+    const uint32_t sorted = wave_sort_desc(lane_max, lane);
+    const uint32_t tau = __shfl(sorted, kTop - 1);
+    // 3. survivors (>= tau; 0 is the empty key)
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+        if (e >= chunks) break;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
+            mine += (c != 0u && c >= tau);
+        }
+    }
+    // exclusive prefix over lanes
+    int incl = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    const int total = __shfl(incl, kWave - 1);
+    uint32_t top;
+    if (total <= kWave) {
+        int pos = incl - mine;
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+            if (e >= chunks) break;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
+                if (c != 0u && c >= tau) ts.survivors[wave][pos++] = c;
+            }
+        }
+        wave_lds_sync();
+        const uint32_t v = lane < total ? ts.survivors[wave][lane] : 0u;
+        top = wave_sort_desc(v, lane);
+    } else {
+        // many equal keys: kTop rounds of "largest composite below the previous"
+        uint32_t prev = 0xFFFFFFFFu, mine_top = 0u;
+        for (int round = 0; round < kTop; ++round) {
+            uint32_t best = 0u;
+#pragma unroll
+            for (int e = 0; e < EMAX; ++e) {
+                if (e >= chunks) break;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
+                    if (c < prev && c > best) best = c;
+                }
+            }
+            best = wave_max_u32(best);
+            if (lane == round) mine_top = best;
+            prev = best;
+        }
+        top = mine_top;
+    }
+    if (lane < kTop) out_top[lane] = top;
+}
+
+template <int EMAX, bool FUSED, int SLOTS>
+__global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
+    __shared__ TileScratch ts;
+    __shared__ VerifyScratch<SLOTS> vs[kWaves];
+    const int tile = blockIdx.x, row = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const bool owned = row < a.owned_rows;
+    const int64_t begin = (int64_t)tile * a.tile_width;
+    const int width_left = (int)((a.width - begin) < a.tile_width ? (a.width - begin) : a.tile_width);
+    const int chunks = (width_left + kChunk - 1) / kChunk;
+    const uint16_t* src = a.logits + (int64_t)row * a.row_stride + begin;
+
+    uint4 raw[EMAX];
+    uint32_t finite_acc = 0;
+    if (owned) {
+        const bool vec = a.vector_loads != 0;
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+            raw[e] = make_uint4(0, 0, 0, 0);
+            if (e >= chunks) continue;
+            const int off = e * kChunk + threadIdx.x * 8;
+            if (vec && off + 8 <= width_left) {
+                raw[e] = *reinterpret_cast<const uint4*>(src + off);
+            } else {
+                uint32_t w[4] = {0, 0, 0, 0};
+                for (int j = 0; j < 8; ++j)
+                    if (off + j < width_left) w[j >> 1] |= (uint32_t)src[off + j] << ((j & 1) * 16);
+                raw[e] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) {
+            if (e >= chunks) break;
+            const int off = e * kChunk + threadIdx.x * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t word = (&raw[e].x)[j >> 1];
+                const uint32_t u = (j & 1) ? (word >> 16) : (word & 0xFFFFu);
+                finite_acc |= (off + j < width_left && nonfinite_bf16(u)) ? 1u : 0u;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) raw[e] = make_uint4(0, 0, 0, 0);
+    }
+    // wave top-kTop of this wave's share, then the workgroup's top-kTop
+    const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
+    tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane, wave,
+                   &ts.wave_top[wave * kTop]);
+    const uint32_t bad = __any(finite_acc != 0);
+    if (lane == 0) ts.flags[wave] = bad;
+    __syncthreads();
+    uint32_t* part = a.partial_keys + ((int64_t)row * a.tiles + tile) * kTop;
+    if (wave == 0) {
+        uint32_t v0 = lane < kTop * kWaves ? ts.wave_top[lane] : 0u;
+        uint32_t v1 = lane + kWave < kTop * kWaves ? ts.wave_top[lane + kWave] : 0u;
+        uint32_t prev = 0xFFFFFFFFu, my = 0u;
+        for (int round = 0; round < kTop; ++round) {
+            uint32_t b = 0u;
+            if (v0 < prev && v0 > b) b = v0;
+            if (v1 < prev && v1 > b) b = v1;
+            b = wave_max_u32(b);
+            if (lane == round) my = b;
+            prev = b;
+        }
+        if (lane < kTop) part[lane] = my;
+        if (lane == 0)
+            a.partial_flags[(int64_t)row * a.tiles + tile] =
+                ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3];
+    }
+    // arrival: the last workgroup of this row group finalises it
+    const int group = row / a.group_rows;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t expected = (uint32_t)(a.group_rows * a.tiles);
+        const uint32_t old = atomicAdd(&a.counters[group], 1u);
+        ts.last = old == expected - 1;
+    }
+    __syncthreads();
+    if (!ts.last) return;
+    __threadfence();
+
+    // ---- finalise the group's rows: merge tiles, publish candidates -------
+    const int row0 = group * a.group_rows;
+    for (int gr = wave; gr < a.group_rows; gr += kWaves) {
+        const int r = row0 + gr;
+        const bool own = r < a.owned_rows;
+        uint32_t bad_row = 0;
+        for (int t = lane; t < a.tiles; t += kWave) bad_row |= a.partial_flags[(int64_t)r * a.tiles + t];
+        bad_row = __any(bad_row != 0);
+        // kTop global winners by (value desc, id asc) over tiles * kTop entries
+        constexpr int kPer = (kMaxTiles * kTop + kWave - 1) / kWave;
+        uint64_t entry[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = lane + q * kWave;
+            entry[q] = 0ull;
+            if (i < a.tiles * kTop) {
+                const uint32_t k32 = a.partial_keys[(int64_t)r * a.tiles * kTop + i];
+                if (k32 != 0u) {
+                    const uint32_t t = (uint32_t)(i / kTop);
+                    const uint32_t id = t * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
+                    entry[q] = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
+                }
+            }
+        }
+        uint64_t prev = ~0ull, my = 0ull;
+        const int want = a.count < kTop ? a.count : kTop;
+        for (int round = 0; round < want; ++round) {
+            uint64_t best = 0ull;
+#pragma unroll
+            for (int q = 0; q < kPer; ++q)
+                if (entry[q] < prev && entry[q] > best) best = entry[q];
+            best = wave_max_u64(best);
+            if (lane == round) my = best;
+            prev = best;
+        }
+        const float temp = a.row_temperatures[r];
+        const bool greedy_pub = temp == 0.0f;
+        const int j = lane;  // capacity <= 64
+        if (j < a.capacity) {
+            uint16_t sc = 0x7FC0u;
+            int64_t id = -1;
+            if (j < a.count && own) {
+                const bool filled = j < want && my != 0ull;
+                const int64_t gid = (int64_t)(0xFFFFFFFFu - (uint32_t)(my & 0xFFFFFFFFu));
+                if (bad_row) {
+                    id = -2;
+                } else if (!greedy_pub) {
+                    if (filled) { sc = a.logits[(int64_t)r * a.row_stride + gid]; id = gid; }
+                } else if (!a.all_random && j == 0 && filled) {
+                    sc = a.logits[(int64_t)r * a.row_stride + gid];
+                    id = gid;
+                }
+            }
+            a.cand_scores[(int64_t)r * a.capacity + j] = sc;
+            a.cand_ids[(int64_t)r * a.capacity + j] = id;
+            if (FUSED) {
+                ts.cand_score[gr][j] = sc;
+                ts.cand_id[gr][j] = id;
+            }
+        }
+    }
+    if (!FUSED) {
+        if (threadIdx.x == 0) a.counters[group] = 0u;
+        return;
+    }
+    __syncthreads();
+    // ---- fused: verify each depth of sequence `group`, merge the prefix ----
+    const int c = group, depth = a.group_rows - 1;
+    for (int d = wave; d < depth; d += kWaves) {
+        const int64_t pi = (int64_t)d * a.c + c;
+        VerifyRow vr;
+        vr.active = c < a.live_rows;
+        vr.rows_ok = true;
+        vr.q_scores = a.q_scores + pi * a.capacity;
+        vr.q_ids = a.q_ids + pi * a.capacity;
+        vr.p0_scores = ts.cand_score[d];
+        vr.p0_ids = ts.cand_id[d];
+        vr.p1_scores = ts.cand_score[d + 1];
+        vr.p1_ids = ts.cand_id[d + 1];
+        vr.q_rank_stride = 0;
+        vr.p_rank_stride = 0;
+        vr.tp = 1;
+        vr.k = a.capacity;
+        vr.block = a.block;
+        vr.draft = vr.active ? a.draft_tokens[pi] : -1;
+        vr.temperature = vr.active ? a.temperatures[pi] : 1.0f;
+        vr.top_p = vr.active ? a.top_ps[pi] : 1.0f;
+        vr.top_k = vr.active ? a.top_ks[pi] : 1;
+        vr.seed = vr.active ? a.seeds[pi] : 0;
+        vr.ordinal = vr.active ? a.ordinals[pi] : 0;
+        vr.uniforms = a.uniforms ? a.uniforms + 2 * pi : nullptr;
+        vr.underfilled = false;
+        verify_wave<SLOTS>(vr, vs[wave], lane, ts.decisions[d]);
+        if (lane == 0) {
+            a.decisions[2 * pi] = ts.decisions[d][0];
+            a.decisions[2 * pi + 1] = ts.decisions[d][1];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int64_t accepted = depth, bonus = ts.decisions[depth - 1][1];
+        bool good = true;
+        for (int d = depth - 1; d >= 0; --d) {
+            const int64_t av = ts.decisions[d][0], tok = ts.decisions[d][1];
+            if (av == 0) { accepted = d; bonus = tok; }
+            good = good && (av == 0 || av == 1) && tok >= 0;
+        }
+        const bool ok = c < a.live_rows && good;
+        a.merged[2 * (int64_t)c] = ok ? accepted : -1;
+        a.merged[2 * (int64_t)c + 1] = ok ? bonus : -1;
+        if (a.emitted) {
+            for (int d = 0; d <= depth; ++d) {
+                int64_t tok = -1;
+                if (ok && d < accepted) tok = a.draft_tokens[(int64_t)d * a.c + c];
+                if (ok && d == accepted) tok = bonus;
+                a.emitted[(int64_t)c * (depth + 1) + d] = tok;
+            }
+        }
+        a.counters[group] = 0u;
+    }
+}
+
+template <int EMAX, bool FUSED>
+hipError_t launch_accept_slots(const AcceptArgs& a, hipStream_t s) {
+    dim3 grid(a.tiles, a.rows), block(kThreads);
+    if (a.block <= 64)
+        accept_kernel<EMAX, FUSED, 1><<<grid, block, 0, s>>>(a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s) {
+    const int chunks = (a.tile_width + kChunk - 1) / kChunk;
+    if (chunks <= 4) return fused ? launch_accept_slots<4, true>(a, s) : launch_accept_slots<4, false>(a, s);
+    if (chunks <= 8) return fused ? launch_accept_slots<8, true>(a, s) : launch_accept_slots<8, false>(a, s);
+    if (chunks <= kMaxTileChunks)
+        return fused ? launch_accept_slots<16, true>(a, s) : launch_accept_slots<16, false>(a, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_verify(const VerifyArgs& a, hipStream_t s) {
+    dim3 grid(a.q_rows), block(kWave);
+    if (a.block <= 64) verify_candidates_kernel<1><<<grid, block, 0, s>>>(a);
+    else if (a.block <= 128) verify_candidates_kernel<2><<<grid, block, 0, s>>>(a);
+    else if (a.block <= 256) verify_candidates_kernel<4><<<grid, block, 0, s>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
+                               int live_rows, int64_t* out, hipStream_t s) {
+    const int blocks = (c + kThreads - 1) / kThreads;
+    merge_prefix_kernel<<<blocks > 0 ? blocks : 1, kThreads, 0, s>>>(decisions, c, depth, live,
+                                                                   live_rows, out);
+    return hipGetLastError();
+}
+
+}  // namespace cubic

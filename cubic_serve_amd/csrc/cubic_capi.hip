@@ -1,0 +1,382 @@
+// C ABI entry points: argument validation, launch planning, kernel dispatch.
+// Declarations and the reference interface each entry replaces are in
+// include/cubic_mi355x.h.
+#include <string>
+#include <cstdio>
+#include <cstdarg>
+
+#include "cubic_mi355x.h"
+#include "cubic_capi_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return CUBIC_OK;
+    return fail(CUBIC_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kKBlock = 128;
+constexpr int kTop = 20;
+constexpr int kChunk = 2048;
+constexpr int kMaxTileChunks = 16;
+constexpr int kMaxTiles = 24;
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// GEMM launch plan: a pure function of (n, k) so every output row sees the
+// same K partition and column grouping whatever m is.
+// ---------------------------------------------------------------------------
+struct GemmPlan {
+    int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
+};
+
+GemmPlan plan_gemm(int64_t n, int64_t k) {
+    GemmPlan p;
+    p.n_tiles = (int)ceil_div(n, 16);
+    p.k_blocks = (int)ceil_div(k, kKBlock);
+    p.tiles_per_wave = 1;
+    for (int j : {4, 2}) {
+        if (ceil_div(p.n_tiles, 4 * j) >= 128) { p.tiles_per_wave = j; break; }
+    }
+    p.col_blocks = (int)ceil_div(p.n_tiles, 4 * p.tiles_per_wave);
+    int split = 512 / p.col_blocks;
+    if (split < 1) split = 1;
+    if (split > 8) split = 8;
+    if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
+    p.blocks_per_split = (int)ceil_div(p.k_blocks, split);
+    p.split = (int)ceil_div(p.k_blocks, p.blocks_per_split);
+    return p;
+}
+
+int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
+    const GemmPlan p = plan_gemm(n, k);
+    if (p.split == 1) return 0;
+    const int64_t counters = (int64_t)p.col_blocks * ceil_div(m, 64) * 4;
+    return align256(counters) + align256((int64_t)p.split * m * n * 4);
+}
+
+int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                int64_t m, int64_t n, int64_t n_split, int64_t k, int bits, int group_in,
+                void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+    if (!x || !codes || !meta || !y0) return fail(CUBIC_EINVAL, "null operand");
+    if (m <= 0 || n <= 0 || k <= 0 || m > (1 << 30) || n > (1 << 30) || k > (1 << 30))
+        return fail(CUBIC_EINVAL, "gemm extents must be positive: m=%lld n=%lld k=%lld",
+                    (long long)m, (long long)n, (long long)k);
+    if (bits < 1 || bits > 8) return fail(CUBIC_ENOTSUP, "bits=%d outside 1..8", bits);
+    if (group_in <= 0 || group_in % 32) return fail(CUBIC_ENOTSUP, "group_in=%d must be a multiple of 32", group_in);
+    if (k % 8 || ldx % 8 || ldx < k || !aligned16(x))
+        return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
+    if (ldy0 < (n_split) || (y1 && ldy1 < n - n_split))
+        return fail(CUBIC_EINVAL, "output leading dimension too small");
+    const GemmPlan p = plan_gemm(n, k);
+    const int64_t need = gemm_workspace(m, n, k);
+    if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
+    if (need && !workspace) return fail(CUBIC_EINVAL, "null workspace");
+    cubic::GemmArgs a = {};
+    a.x = (const uint16_t*)x;
+    a.codes = codes;
+    a.meta = meta;
+    a.y0 = (uint16_t*)y0;
+    a.y1 = (uint16_t*)y1;
+    a.ldx = ldx;
+    a.ldy0 = ldy0;
+    a.ldy1 = ldy1;
+    a.m = (int)m;
+    a.n = (int)n;
+    a.k = (int)k;
+    a.n_split = (int)n_split;
+    a.bits = bits;
+    a.group_in = group_in;
+    a.k_blocks = p.k_blocks;
+    a.groups_k = (int)ceil_div(k, group_in);
+    a.split = p.split;
+    a.blocks_per_split = p.blocks_per_split;
+    a.n_tiles = p.n_tiles;
+    a.tiles_per_wave = p.tiles_per_wave;
+    if (p.split > 1) {
+        const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, 64) * 4);
+        a.counters = (uint32_t*)workspace;
+        a.partials = (float*)((char*)workspace + counters);
+    }
+    return hip_status(cubic::launch_gemm(a, (hipStream_t)stream), "cubic_gemm launch");
+}
+
+// ---------------------------------------------------------------------------
+// Candidate tiling: enough (row, tile) workgroups to cover the chip.
+// ---------------------------------------------------------------------------
+struct TilePlan {
+    int tiles, tile_width;
+};
+
+bool plan_tiles(int rows, int width, TilePlan* out) {
+    if (width <= 0 || rows <= 0) return false;
+    int target = (int)ceil_div(1024, rows);
+    if (target < 1) target = 1;
+    if (target > kMaxTiles) target = kMaxTiles;
+    int64_t tw = ceil_div(ceil_div(width, target), kChunk) * kChunk;
+    const int64_t min_tw = ceil_div(ceil_div(width, kMaxTiles), kChunk) * kChunk;
+    if (tw < min_tw) tw = min_tw;
+    if (tw > (int64_t)kChunk * kMaxTileChunks) return false;
+    out->tile_width = (int)tw;
+    out->tiles = (int)ceil_div(width, tw);
+    return out->tiles <= kMaxTiles;
+}
+
+int64_t accept_workspace(int rows, int groups, int width) {
+    TilePlan t;
+    if (!plan_tiles(rows, width, &t)) return -1;
+    return align256((int64_t)groups * 4) + align256((int64_t)rows * t.tiles * kTop * 4) +
+           align256((int64_t)rows * t.tiles * 4);
+}
+
+void carve_accept(void* ws, int rows, int groups, int tiles, cubic::AcceptArgs& a) {
+    char* p = (char*)ws;
+    a.counters = (uint32_t*)p;
+    p += align256((int64_t)groups * 4);
+    a.partial_keys = (uint32_t*)p;
+    p += align256((int64_t)rows * tiles * kTop * 4);
+    a.partial_flags = (uint32_t*)p;
+}
+
+int next_pow2(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cubic_abi_version(void) { return 1; }
+
+const char* cubic_last_error(void) { return g_error.c_str(); }
+
+int cubic_prepared_words(int64_t n, int64_t k, int bits, int group_in, int64_t* code_words,
+                         int64_t* meta_words) {
+    if (n <= 0 || k <= 0 || bits < 1 || bits > 8 || group_in <= 0 || group_in % 32)
+        return fail(CUBIC_EINVAL, "invalid prepared geometry");
+    const int64_t n_tiles = ceil_div(n, 16), k_blocks = ceil_div(k, kKBlock);
+    if (code_words) *code_words = n_tiles * k_blocks * 64 * bits;
+    if (meta_words) *meta_words = n_tiles * ceil_div(k, group_in) * 16 * 2;
+    return CUBIC_OK;
+}
+
+int64_t cubic_prepare_scratch_bytes(int64_t n, int64_t k, int group_in) {
+    if (n <= 0 || k <= 0 || group_in <= 0) return -1;
+    const int64_t groups = n * ceil_div(k, group_in);
+    return align256(groups * 4) + 2 * align256(groups * 2);
+}
+
+int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void* m1,
+                         const void* m2, const void* g0, const void* g1, const void* g2,
+                         const int32_t* part_of_row, int64_t n, int64_t k, int bits,
+                         int group_in, int group_out, void* expanded, int64_t expanded_bytes,
+                         uint32_t* codes, uint32_t* meta, void* stream) {
+    if (!packed || !m0 || !m1 || !codes || !meta || !expanded)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (fmt < 0 || fmt > 2) return fail(CUBIC_ENOTSUP, "unknown metadata format %d", fmt);
+    if (n <= 0 || k <= 0 || bits < 1 || bits > 8) return fail(CUBIC_EINVAL, "invalid geometry");
+    if (group_in <= 0 || group_in % 32) return fail(CUBIC_ENOTSUP, "group_in=%d must be a multiple of 32", group_in);
+    if (group_out <= 0 || n % group_out) return fail(CUBIC_EINVAL, "group_out must divide n");
+    if (fmt != 0 && !part_of_row) return fail(CUBIC_EINVAL, "format %d needs part_of_row", fmt);
+    if (fmt == 1 && (!g0 || !g1 || !g2)) return fail(CUBIC_EINVAL, "format 1 needs the partition globals");
+    if (fmt != 1 && !m2) return fail(CUBIC_EINVAL, "format %d needs its third metadata tensor", fmt);
+    const int64_t need = cubic_prepare_scratch_bytes(n, k, group_in);
+    if (expanded_bytes < need) return fail(CUBIC_EWORKSPACE, "prepare scratch %lld < %lld", (long long)expanded_bytes, (long long)need);
+    const int64_t groups_k = ceil_div(k, group_in);
+    const int64_t groups = n * groups_k;
+    char* p = (char*)expanded;
+    float* scale = (float*)p;
+    uint16_t* av = (uint16_t*)(p + align256(groups * 4));
+    uint16_t* bv = (uint16_t*)(p + align256(groups * 4) + align256(groups * 2));
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = cubic::launch_expand_metadata(fmt, m0, m1, m2, g0, g1, g2, part_of_row, n,
+                                                 groups_k, group_out, scale, av, bv, s);
+    if (e != hipSuccess) return hip_status(e, "metadata expansion");
+    e = cubic::launch_prepare(packed, scale, av, bv, n, k, bits, group_in, codes, meta, s);
+    return hip_status(e, "weight preparation");
+}
+
+int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits) {
+    if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
+    return gemm_workspace(m, n, k);
+}
+
+int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+               int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
+               void* workspace, int64_t workspace_bytes, void* stream) {
+    return gemm_common(x, ldx, codes, meta, m, n, n, k, bits, group_in, y, ldy, nullptr, 0,
+                       workspace, workspace_bytes, stream);
+}
+
+int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
+                       void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+    if (!y1 || n0 <= 0 || n1 <= 0) return fail(CUBIC_EINVAL, "grouped gemm needs two members");
+    return gemm_common(x, ldx, codes, meta, m, n0 + n1, n0, k, bits, group_in, y0, ldy0, y1,
+                       ldy1, workspace, workspace_bytes, stream);
+}
+
+int64_t cubic_candidates_workspace_bytes(int rows, int width) {
+    return accept_workspace(rows, rows, width);
+}
+
+int cubic_candidates(const void* logits, int64_t row_stride, int rows, int width,
+                     const float* temperatures, int owned_rows, int count, int capacity,
+                     int all_random, void* scores, int64_t* ids, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
+    if (!logits || !temperatures || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "null operand");
+    if (rows <= 0 || width <= 0 || row_stride < width) return fail(CUBIC_EINVAL, "invalid logits geometry");
+    if (owned_rows < 0 || owned_rows > rows) return fail(CUBIC_EINVAL, "owned_rows outside 0..rows");
+    if (count < 1 || count > kTop || capacity < count || capacity > 64)
+        return fail(CUBIC_EINVAL, "need 1 <= count <= 20 and count <= capacity <= 64");
+    TilePlan t;
+    if (!plan_tiles(rows, width, &t)) return fail(CUBIC_ENOTSUP, "vocabulary width %d too large", width);
+    const int64_t need = accept_workspace(rows, rows, width);
+    if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "candidate workspace %lld < %lld", (long long)workspace_bytes, (long long)need);
+    cubic::AcceptArgs a = {};
+    a.logits = (const uint16_t*)logits;
+    a.row_stride = row_stride;
+    a.rows = rows;
+    a.width = width;
+    a.tiles = t.tiles;
+    a.tile_width = t.tile_width;
+    a.vector_loads = aligned16(logits) && row_stride % 8 == 0;
+    a.row_temperatures = temperatures;
+    a.owned_rows = owned_rows;
+    a.count = count;
+    a.capacity = capacity;
+    a.all_random = all_random;
+    a.cand_scores = (uint16_t*)scores;
+    a.cand_ids = ids;
+    a.group_rows = 1;
+    carve_accept(workspace, rows, rows, t.tiles, a);
+    return hip_status(cubic::launch_accept(a, false, (hipStream_t)stream), "cubic_candidates launch");
+}
+
+int cubic_verify_candidates(const void* q_scores, const int64_t* q_ids, const void* p_scores,
+                            const int64_t* p_ids, const int32_t* target_rows,
+                            const int64_t* draft_tokens, const float* temperatures,
+                            const float* top_ps, const int64_t* top_ks, const int64_t* seeds,
+                            const int64_t* ordinals, const float* uniforms,
+                            const uint8_t* constrained_rows, int allow_underfilled, int tp,
+                            int q_rows, int p_rows, int k, int active_rows, int64_t* decisions,
+                            void* stream) {
+    if (!q_scores || !q_ids || !p_scores || !p_ids || !target_rows || !draft_tokens ||
+        !temperatures || !top_ps || !top_ks || !seeds || !ordinals || !decisions)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (tp < 1 || tp > 8 || k < 1 || k > 20) return fail(CUBIC_EINVAL, "speculative candidates require 1 <= tp <= 8, 1 <= k <= 20");
+    if (q_rows < 1 || p_rows < 1 || active_rows < 1 || active_rows > q_rows)
+        return fail(CUBIC_EINVAL, "speculative row buffers differ from proposal capacity");
+    cubic::VerifyArgs a = {};
+    a.q_scores = (const uint16_t*)q_scores;
+    a.q_ids = q_ids;
+    a.p_scores = (const uint16_t*)p_scores;
+    a.p_ids = p_ids;
+    a.target_rows = target_rows;
+    a.draft_tokens = draft_tokens;
+    a.temperatures = temperatures;
+    a.top_ps = top_ps;
+    a.top_ks = top_ks;
+    a.seeds = seeds;
+    a.ordinals = ordinals;
+    a.uniforms = uniforms;
+    a.constrained_rows = constrained_rows;
+    a.decisions = decisions;
+    a.tp = tp;
+    a.q_rows = q_rows;
+    a.p_rows = p_rows;
+    a.k = k;
+    a.block = next_pow2(tp * k);
+    a.active_rows = active_rows;
+    a.allow_underfilled = allow_underfilled;
+    return hip_status(cubic::launch_verify(a, (hipStream_t)stream), "cubic_verify_candidates launch");
+}
+
+int cubic_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
+                       int live_rows, int64_t* out, void* stream) {
+    if (!decisions || !out) return fail(CUBIC_EINVAL, "null operand");
+    if (c < 1 || depth < 1) return fail(CUBIC_EINVAL, "merge needs c >= 1 and depth >= 1");
+    return hip_status(cubic::launch_merge_prefix(decisions, c, depth, live, live_rows, out,
+                                                 (hipStream_t)stream), "cubic_merge_prefix launch");
+}
+
+int64_t cubic_accept_workspace_bytes(int c, int depth, int width) {
+    if (c < 1 || depth < 1 || depth > 8) return -1;
+    return accept_workspace(c * (depth + 1), c, width);
+}
+
+int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int depth,
+                 int live_rows, const float* row_temperatures, const void* q_scores,
+                 const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
+                 const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                 const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
+                 void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
+                 int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!logits || !row_temperatures || !q_scores || !q_ids || !draft_tokens || !temperatures ||
+        !top_ps || !top_ks || !seeds || !ordinals || !cand_scores || !cand_ids || !decisions ||
+        !merged || !workspace)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (c < 1 || depth < 1 || depth > 8) return fail(CUBIC_EINVAL, "need c >= 1 and 1 <= depth <= 8");
+    if (live_rows < 0 || live_rows > c) return fail(CUBIC_EINVAL, "live_rows outside 0..c");
+    if (capacity < 1 || capacity > kTop) return fail(CUBIC_EINVAL, "capacity must be 1..20");
+    if (width <= 0 || row_stride < width) return fail(CUBIC_EINVAL, "invalid logits geometry");
+    const int rows = c * (depth + 1);
+    TilePlan t;
+    if (!plan_tiles(rows, width, &t)) return fail(CUBIC_ENOTSUP, "vocabulary width %d too large", width);
+    const int64_t need = accept_workspace(rows, c, width);
+    if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "accept workspace %lld < %lld", (long long)workspace_bytes, (long long)need);
+    cubic::AcceptArgs a = {};
+    a.logits = (const uint16_t*)logits;
+    a.row_stride = row_stride;
+    a.rows = rows;
+    a.width = width;
+    a.tiles = t.tiles;
+    a.tile_width = t.tile_width;
+    a.vector_loads = aligned16(logits) && row_stride % 8 == 0;
+    a.row_temperatures = row_temperatures;
+    a.owned_rows = live_rows * (depth + 1);
+    a.count = capacity;
+    a.capacity = capacity;
+    a.all_random = 0;
+    a.cand_scores = (uint16_t*)cand_scores;
+    a.cand_ids = cand_ids;
+    a.group_rows = depth + 1;
+    a.c = c;
+    a.live_rows = live_rows;
+    a.block = next_pow2(capacity);
+    a.q_scores = (const uint16_t*)q_scores;
+    a.q_ids = q_ids;
+    a.draft_tokens = draft_tokens;
+    a.temperatures = temperatures;
+    a.top_ps = top_ps;
+    a.top_ks = top_ks;
+    a.seeds = seeds;
+    a.ordinals = ordinals;
+    a.uniforms = uniforms;
+    a.decisions = decisions;
+    a.merged = merged;
+    a.emitted = emitted;
+    carve_accept(workspace, rows, c, t.tiles, a);
+    return hip_status(cubic::launch_accept(a, true, (hipStream_t)stream), "cubic_accept launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+// Kernel argument blocks shared between the C-ABI entry points (cubic_capi.cpp)
+// and the kernels.  Not part of the public interface (include/cubic_mi355x.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cubic {
+
+struct AcceptArgs {
+    const uint16_t* logits;       // [rows, row_stride] bf16
+    int64_t row_stride;           // elements
+    int rows, width, tiles, tile_width, vector_loads;
+    const float* row_temperatures;  // [rows]: 0 = greedy publication
+    int owned_rows, count, capacity, all_random;
+    uint16_t* cand_scores;        // [rows, capacity] bf16
+    int64_t* cand_ids;            // [rows, capacity]
+    int group_rows;               // rows finalised together (1, or depth+1 when fused)
+    uint32_t* counters;           // [rows / group_rows], zero between launches
+    uint32_t* partial_keys;       // [rows, tiles, 20]
+    uint32_t* partial_flags;      // [rows, tiles]
+    // fused verify (group = one sequence of depth+1 target rows)
+    int c, live_rows, block;
+    const uint16_t* q_scores;     // [depth, c, capacity] bf16
+    const int64_t* q_ids;
+    const int64_t* draft_tokens;  // [depth, c]
+    const float* temperatures;    // [depth, c]
+    const float* top_ps;
+    const int64_t* top_ks;
+    const int64_t* seeds;
+    const int64_t* ordinals;
+    const float* uniforms;        // [depth, c, 2] or null
+    int64_t* decisions;           // [depth, c, 2]
+    int64_t* merged;              // [c, 2]
+    int64_t* emitted;             // [c, depth + 1] or null
+};
+
+struct VerifyArgs {
+    const uint16_t* q_scores;  // [tp, q_rows, k] bf16
+    const int64_t* q_ids;
+    const uint16_t* p_scores;  // [tp, p_rows, k] bf16
+    const int64_t* p_ids;
+    const int32_t* target_rows;
+    const int64_t* draft_tokens;
+    const float* temperatures;
+    const float* top_ps;
+    const int64_t* top_ks;
+    const int64_t* seeds;
+    const int64_t* ordinals;
+    const float* uniforms;        // [q_rows, 2] or null
+    const uint8_t* constrained_rows;  // [q_rows] bool or null
+    int64_t* decisions;           // [q_rows, 2]
+    int tp, q_rows, p_rows, k, block, active_rows, allow_underfilled;
+};
+
+struct GemmArgs {
+    const uint16_t* x;            // [m, k] bf16, row stride ldx
+    const uint32_t* codes;        // prepared code tiles
+    const uint32_t* meta;         // prepared (scale, a|b) per (column, group)
+    uint16_t* y0;                 // columns [0, n_split)
+    uint16_t* y1;                 // columns [n_split, n) or null
+    float* partials;              // split-K FP32 partials or null
+    uint32_t* counters;           // split-K arrival counters or null
+    int64_t ldx, ldy0, ldy1;
+    int m, n, k, n_split;
+    int bits, group_in;
+    int k_blocks, groups_k;       // ceil(k / 128), ceil(k / group_in)
+    int split, blocks_per_split;  // K partitions and k-blocks per partition
+    int n_tiles;                  // ceil(n / 16)
+    int tiles_per_wave;           // J: 16-column tiles per wave (1, 2, 4)
+    // routed experts (MoE): rows of x gathered through row_map, one expert per m-block
+    const int32_t* row_map;       // [padded routes] source token row, -1 = padding
+    const int32_t* block_expert;  // [m-blocks] expert of each 16-route block
+    int64_t expert_code_stride, expert_meta_stride;  // uint32 words per expert
+    int routed_blocks;
+};
+
+hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s);
+hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
+hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
+                               int live_rows, int64_t* out, hipStream_t s);
+hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t* a,
+                          const uint16_t* b, int64_t n, int64_t k, int bits, int group_in,
+                          uint32_t* codes, uint32_t* meta, hipStream_t s);
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// fmt 0: m0 scale f32, m1 a f16, m2 b f16; fmt 1: m0 scale i8, m1 ab u8, g0..g2
+// globals f32; fmt 2: m0 metadata u16, m1 curve_a f16, m2 curve_b f16.
+hipError_t launch_expand_metadata(int fmt, const void* m0, const void* m1, const void* m2,
+                                  const void* g0, const void* g1, const void* g2,
+                                  const int32_t* part_of_row,
+                                  int64_t n, int64_t groups_k, int group_out, float* scale,
+                                  uint16_t* a, uint16_t* b, hipStream_t s);
+
+}  // namespace cubic

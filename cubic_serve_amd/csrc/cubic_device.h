@@ -5,6 +5,7 @@
 // binary32 operations.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <stdint.h>
 
 namespace cubic {
@@ -23,8 +24,9 @@ __device__ __forceinline__ uint32_t float_to_bf16_bits(float f) {
 // Two binary32 -> packed bfloat16 pair (lo, hi), RNE, one instruction on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-    bf16x2_t v = __builtin_amdgcn_cvt_pk_bf16_f32(lo, hi);
-    return __builtin_bit_cast(uint32_t, v);
+    typedef __attribute__((ext_vector_type(2))) float float2_t;
+    const float2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));  // v_cvt_pk_bf16_f32
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {

@@ -1,0 +1,168 @@
+/*
+ * cubic_mi355x.h -- C ABI of the MI355X (gfx950) MTP verify-step library.
+ *
+ * Plain pointers and sizes only.  Every pointer argument named *device* data
+ * is a device address on the current HIP device; `stream` is a hipStream_t
+ * (NULL = the default stream).  Every entry point returns 0 on success or a
+ * negative CUBIC_E* code; cubic_last_error() then describes the failure.
+ * Nothing here allocates device memory except cubic_* functions documented as
+ * doing so (none do): callers own weights, outputs and workspaces.
+ *
+ * Reference paths are relative to src/cubic_serve/ of QuantTrio/cubic-serve.
+ */
+#ifndef CUBIC_MI355X_H
+#define CUBIC_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define CUBIC_API __attribute__((visibility("default")))
+#else
+#define CUBIC_API
+#endif
+
+#define CUBIC_OK 0
+#define CUBIC_EINVAL (-1)      /* argument outside the admitted ABI (shape, dtype, size) */
+#define CUBIC_ENOTSUP (-2)     /* geometry not admitted by this kernel family */
+#define CUBIC_EHIP (-3)        /* HIP runtime / launch failure */
+#define CUBIC_EWORKSPACE (-4)  /* workspace smaller than the planned size */
+
+/* Metadata formats (quantization/extensions/cubic/checkpoint.py:38-46). */
+#define CUBIC_FMT_F32_SCALE_F16_AB 0  /* "float32-scale-float16-ab" */
+#define CUBIC_FMT_I8_SCALE_I4_AB 1    /* "int8-scale-int4-ab-global-fp32" */
+#define CUBIC_FMT_E5M9_CURVE2 2       /* "e5m9-scale-curve2-tensor-fp16" */
+
+CUBIC_API int cubic_abi_version(void);
+CUBIC_API const char* cubic_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Cubic weight preparation (load time).
+ * Replaces the format-prepared derivatives of quantization/extensions/cubic/
+ * marlin.py:38-81 (_prepare: repack_signed_codes + prepare_metadata) and
+ * marlin_metadata.py:35-100.
+ *
+ * cubic_prepared_words: sizes (in uint32 words) of the prepared code stream
+ * and metadata for an [n, k] matrix.
+ * cubic_prepare_weight: device payload -> prepared (codes, meta).
+ *   packed        uint8 [n, ceil(k*bits/8)]    weight_packed
+ *   fmt 0: m0 = weight_scale f32, m1 = weight_a f16, m2 = weight_b f16   [n/go, ceil(k/gi)]
+ *   fmt 1: m0 = weight_scale i8, m1 = weight_ab u8; g0..g2 = *_global f32 [partitions]
+ *   fmt 2: m0 = weight_metadata u16; m1 = weight_curve_a f16, m2 = weight_curve_b f16 [partitions, 4]
+ *   part_of_row   int32 [n] partition index of each output row (fmt 1, 2; may be NULL for fmt 0)
+ *   expanded      device scratch of cubic_prepare_scratch_bytes() bytes
+ * Admission (quantization/extensions/cubic/marlin.py:256-336 analogue):
+ *   1 <= bits <= 8, group_in % 32 == 0, k % 8 == 0, group_out divides n.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_prepared_words(int64_t n, int64_t k, int bits, int group_in, int64_t* code_words,
+                         int64_t* meta_words);
+CUBIC_API int64_t cubic_prepare_scratch_bytes(int64_t n, int64_t k, int group_in);
+CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void* m1,
+                         const void* m2, const void* g0, const void* g1, const void* g2,
+                         const int32_t* part_of_row, int64_t n, int64_t k, int bits,
+                         int group_in, int group_out, void* expanded, int64_t expanded_bytes,
+                         uint32_t* codes, uint32_t* meta, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Cubic WNA16 GEMM: y = x . decode(W)^T, bf16 in/out, FP32 accumulation.
+ * Replaces the Marlin launch plus _merge_dense_partials of
+ * quantization/extensions/cubic/marlin.py:377-521 (bind_planned_linear :339)
+ * and the small-row kernel of quantization/common/small_rows.cu:94-241.
+ *
+ * cubic_gemm_workspace_bytes: workspace for (m, n, k); 0 when no K split.
+ *   The workspace must be zero-filled before its first use; every launch
+ *   leaves it zero again.  One workspace per concurrently running launch.
+ * cubic_gemm: single output y[m, ldy] (columns n).
+ * cubic_gemm_grouped: two members sharing x (gate/up), prepared as one
+ *   [n0 + n1, k] matrix; columns < n0 go to y0, the rest to y1
+ *   (bind_linear_group, ops/cuda/linear/quantized.py:445-507;
+ *   cubic/marlin.py:347 bind_planned_grouped).
+ * x: bf16 [m, ldx], 16-byte aligned, ldx % 8 == 0.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits);
+CUBIC_API int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+               int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
+               void* workspace, int64_t workspace_bytes, void* stream);
+CUBIC_API int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
+                       void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Candidate preparation: vocab logits -> top-`count` candidates per row.
+ * Replaces LocalCandidatePlan.launch (ops/cuda/sampling/local_candidates.py:
+ * 206-226: torch.topk + candidate_partial/candidate_publish,
+ * local_candidates.cu:19-146) and the greedy argmax (greedy.cu:14-78).
+ *   logits        bf16 [rows, row_stride], width <= row_stride visible columns
+ *   temperatures  f32 [rows]; 0 = greedy row (slot 0 = argmax, lowest id on ties)
+ *   scores/ids    bf16 / int64 [rows, capacity]; padding (NaN, -1); rows with a
+ *                 non-finite logit publish id -2 in every counted slot
+ *   1 <= count <= 20, count <= capacity <= 64; ties ordered by ascending id.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int64_t cubic_candidates_workspace_bytes(int rows, int width);
+CUBIC_API int cubic_candidates(const void* logits, int64_t row_stride, int rows, int width,
+                     const float* temperatures, int owned_rows, int count, int capacity,
+                     int all_random, void* scores, int64_t* ids, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * K1 speculative verification over [tp, rows, k] candidates.
+ * Replaces verify_one_draft_candidates (ops/cuda/sampling/speculative.py:
+ * 222-328, kernel :46-219); same operand meanings and dtypes:
+ *   q_scores/p_scores bf16, q_ids/p_ids int64, target_rows int32 [q_rows],
+ *   draft_tokens/top_ks/seeds/ordinals int64 [q_rows], temperatures/top_ps f32,
+ *   uniforms f32 [q_rows, 2] or NULL (Philox draws), constrained_rows bool or
+ *   NULL, decisions int64 [q_rows, 2] = (accepted, next) or (-1, -1).
+ *   1 <= tp <= 8, 1 <= k <= 20, 1 <= active_rows <= q_rows.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_verify_candidates(const void* q_scores, const int64_t* q_ids, const void* p_scores,
+                            const int64_t* p_ids, const int32_t* target_rows,
+                            const int64_t* draft_tokens, const float* temperatures,
+                            const float* top_ps, const int64_t* top_ks, const int64_t* seeds,
+                            const int64_t* ordinals, const float* uniforms,
+                            const uint8_t* constrained_rows, int allow_underfilled, int tp,
+                            int q_rows, int p_rows, int k, int active_rows, int64_t* decisions,
+                            void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Accepted-prefix merge.  Replaces merge_prefix (executor/draft_graph.py:
+ * 146-157): decisions int64 [depth, c, 2] -> out int64 [c, 2] =
+ * (accepted length, bonus token) or (-1, -1).  live: device int32 row count
+ * (the reference's ctx[0]) or NULL to use live_rows.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
+                       int live_rows, int64_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused verify from logits: candidates of the c*(depth+1) target rows, then
+ * verification of every depth, then the prefix merge -- the composition of
+ * LocalCandidatePlan.launch, verify_one_draft_candidates per depth and
+ * merge_prefix in finish_review (executor/draft_graph.py:1034-1067), in one
+ * launch and one pass over the logits.  TP = 1.
+ *   logits            bf16 [c*(depth+1), row_stride], row c*(depth+1)+d
+ *   row_temperatures  f32 [c*(depth+1)] candidate publication temperatures
+ *   q_scores/q_ids    bf16/int64 [depth, c, capacity] draft candidates
+ *   draft_tokens, top_ks, seeds, ordinals  int64 [depth, c];
+ *   temperatures, top_ps f32 [depth, c]; uniforms f32 [depth, c, 2] or NULL
+ *   cand_scores/ids   bf16/int64 [c*(depth+1), capacity] published candidates
+ *   decisions int64 [depth, c, 2]; merged int64 [c, 2]; emitted int64
+ *   [c, depth+1] (accepted drafts then the bonus token, -1 padded) or NULL.
+ *   1 <= depth <= 8, 1 <= capacity <= 20.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int64_t cubic_accept_workspace_bytes(int c, int depth, int width);
+CUBIC_API int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int depth,
+                 int live_rows, const float* row_temperatures, const void* q_scores,
+                 const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
+                 const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                 const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
+                 void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
+                 int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUBIC_MI355X_H */

@@ -1,0 +1,50 @@
+"""CPU checks of the C ABI library: it loads, exports every declared symbol,
+and its host-side planning entry points answer without a GPU."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from cubic_serve_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "cubic_mi355x.h"
+
+
+def declared_symbols() -> list[str]:
+    return re.findall(r"^CUBIC_API [^(]*?\b(cubic_\w+)\(", HEADER.read_text(), flags=re.M)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    names = declared_symbols()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.SIGNATURES), "ctypes signatures drift from the header"
+    assert lib.cubic_abi_version() == 1
+
+
+def test_host_planning_entry_points():
+    lib = _native.lib()
+    cw, mw = _native.ctypes.c_int64(), _native.ctypes.c_int64()
+    _native.call("cubic_prepared_words", 151936, 4096, 4, 128, _native.ctypes.byref(cw),
+                 _native.ctypes.byref(mw))
+    assert cw.value * 4 == 151936 * 4096 * 4 // 8       # 4-bit codes, no padding
+    assert mw.value * 4 == 151936 * (4096 // 128) * 8   # 8 bytes per group
+    assert lib.cubic_gemm_workspace_bytes(64, 151936, 4096, 4) == 0   # no K split for the lm_head
+    assert lib.cubic_gemm_workspace_bytes(64, 4096, 12288, 4) > 0     # down projection splits K
+    assert lib.cubic_gemm_workspace_bytes(1, 4096, 12288, 4) < lib.cubic_gemm_workspace_bytes(64, 4096, 12288, 4)
+    assert lib.cubic_accept_workspace_bytes(32, 1, 151936) > 0
+    assert lib.cubic_accept_workspace_bytes(32, 9, 151936) == -1      # depth above 8
+    assert lib.cubic_candidates_workspace_bytes(64, 10**7) == -1      # vocabulary too wide
+
+
+def test_invalid_arguments_fail_before_any_launch():
+    with pytest.raises(ValueError, match="count"):
+        _native.call("cubic_candidates", 16, 100, 2, 100, 16, 2, 21, 21, 0, 16, 16, 16, 1 << 20, None)
+    with pytest.raises(ValueError, match="tp"):
+        _native.call("cubic_verify_candidates", *([16] * 13), 0, 9, 4, 8, 20, 4, 16, None)
+    with pytest.raises(ValueError, match="group_in"):
+        _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 100, 16, 4096, None, 0, None)

@@ -1,0 +1,182 @@
+"""GPU parity: the Cubic GEMM against the CPU oracle.
+
+* one-hot identity contraction: the GEMM output is the decoded weight matrix,
+  bit for bit equal to bf16(decode_cubic) (tests/ops/test_cubic_marlin.py:285-318
+  method, zero signs canonicalised);
+* every output inside the FP64 enclosure of guardrail/quantization.py:176-320,
+  with max-abs and relative-L2 error reported against the oracle's FP32 GEMM;
+* bitwise invariance of a row's output to M and to row permutation;
+* grouped (gate/up) launch equal to the separate launches.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cubic_serve_amd import linear, quantization as qz
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+FMTS = (qz.FMT_F32, qz.FMT_I8, qz.FMT_CURVE2)
+
+
+def to_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def np_payload(m: qz.QuantizedMatrix) -> dict:
+    return {k: v.cpu().numpy() for k, v in m.payload.items()}
+
+
+def random_matrix(n, k, bits, group_in, fmt, seed, partitions=()):
+    """Random payload of every metadata format (reference test style)."""
+    g = torch.Generator().manual_seed(seed)
+    rows_bytes = math.ceil(k * bits / 8)
+    packed = torch.randint(0, 256, (n, rows_bytes), generator=g, dtype=torch.int32).to(torch.uint8)
+    groups = (n, math.ceil(k / group_in))
+    parts = partitions or (n,)
+    if fmt == qz.FMT_F32:
+        payload = {"weight_packed": packed,
+                   "weight_scale": torch.rand(groups, generator=g) * 0.05,
+                   "weight_a": (torch.rand(groups, generator=g) * 1.5 - 0.25).half(),
+                   "weight_b": (torch.rand(groups, generator=g) - 0.5).half()}
+    elif fmt == qz.FMT_I8:
+        payload = {"weight_packed": packed,
+                   "weight_scale": torch.randint(0, 128, groups, generator=g, dtype=torch.int32).to(torch.int8),
+                   "weight_ab": torch.randint(0, 256, groups, generator=g, dtype=torch.int32).to(torch.uint8),
+                   "weight_scale_global": torch.rand(len(parts), generator=g) * 1e-3 + 1e-4,
+                   "weight_a_global": torch.rand(len(parts), generator=g) * 0.1,
+                   "weight_b_global": torch.rand(len(parts), generator=g) * 0.1}
+    else:
+        md = torch.randint(0, 1 << 16, groups, generator=g, dtype=torch.int32) & 0xDFFF
+        payload = {"weight_packed": packed,
+                   "weight_metadata": md.to(torch.uint16),
+                   "weight_curve_a": (torch.rand((len(parts), 4), generator=g) * 1.5).half(),
+                   "weight_curve_b": (torch.rand((len(parts), 4), generator=g) - 0.5).half()}
+    enc = qz.QuantizationScheme(qz.CUBIC_FORMAT, bits, group_in, 1, fmt)
+    return qz.QuantizedMatrix(payload, enc, (n, k), tuple(partitions))
+
+
+def oracle_decode_bits(oracle, m: qz.QuantizedMatrix) -> np.ndarray:
+    e = m.encoding
+    return oracle.decode_bf16(np_payload(m), e.bits, e.metadata, m.shape, e.group_in,
+                              e.group_out, m.partitions)
+
+
+def canon_zero(bits: np.ndarray) -> np.ndarray:
+    out = bits.copy()
+    out[out == 0x8000] = 0
+    return out
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("fmt", FMTS)
+def test_identity_contraction_is_exact_decode(oracle, bits, fmt):
+    n, k, gi = 72, 256, 128 if bits % 2 else 64
+    print(f"identity bits={bits} fmt={fmt} gi={gi}", flush=True)
+    m = random_matrix(n, k, bits, gi, fmt, seed=bits * 10 + FMTS.index(fmt), partitions=(40, 32))
+    x = torch.eye(k, dtype=torch.bfloat16, device=DEV)
+    y = linear.PackedLinearOperators().linear(x, m.to(DEV))
+    torch.cuda.synchronize()
+    got = to_bits(y.T.contiguous())        # [n, k] decoded weights
+    want = oracle_decode_bits(oracle, m)
+    assert np.array_equal(canon_zero(got), canon_zero(want))
+
+
+@pytest.mark.parametrize("k,gi", [(200, 32), (384, 256), (136, 128)])
+def test_identity_partial_groups_and_k_tails(oracle, k, gi):
+    m = random_matrix(33, k, 4, gi, qz.FMT_F32, seed=k)
+    x = torch.eye(k, dtype=torch.bfloat16, device=DEV)
+    y = linear.PackedLinearOperators().linear(x, m.to(DEV))
+    got = to_bits(y.T.contiguous())
+    assert np.array_equal(canon_zero(got), canon_zero(oracle_decode_bits(oracle, m)))
+
+
+def _check_linear(oracle, m: qz.QuantizedMatrix, x: torch.Tensor, y: torch.Tensor) -> dict:
+    w = oracle_decode_bits(oracle, m)
+    xb, yb = to_bits(x), to_bits(y)
+    report = oracle.check_linear_enclosure(xb, w, yb)
+    _, ref32 = oracle.linear_bf16(xb, w)
+    yf = oracle.bf16_bits_to_f32(yb).astype(np.float64)
+    diff = yf - ref32
+    report["vs_oracle_max_abs"] = float(np.abs(diff).max())
+    report["vs_oracle_rel_l2"] = float(np.linalg.norm(diff) / max(np.linalg.norm(ref32), 1e-30))
+    print(report, flush=True)
+    assert report["vs_oracle_rel_l2"] < 1e-2  # bf16 output rounding dominates (2^-9 relative)
+    return report
+
+
+@pytest.mark.parametrize("mrows", [1, 2, 3, 8, 17, 33, 64, 65, 130])
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_enclosure_random_activations(oracle, mrows, bits):
+    n, k = 200, 1024
+    w = torch.randn((n, k), generator=torch.Generator().manual_seed(mrows)) * 0.02
+    m = qz.quantize_cubic(w, bits=bits, group_in=128)
+    x = torch.randn((mrows, k), generator=torch.Generator().manual_seed(99)).to(torch.bfloat16).to(DEV)
+    y = linear.PackedLinearOperators().linear(x, m.to(DEV))
+    _check_linear(oracle, m, x, y)
+
+
+def test_split_k_path_enclosure_and_repeatability(oracle):
+    # small N, long K: the plan splits K and merges partials in order
+    n, k = 64, 12288
+    m = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(5)) * 0.02, 4)
+    x = torch.randn((64, k), generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(DEV)
+    out = torch.empty((64, n), dtype=torch.bfloat16, device=DEV)
+    binding = linear.PackedLinearOperators().bind_linear(x, m.to(DEV), out)
+    assert binding.scratch, "expected a split-K workspace"
+    binding.launch()
+    first = out.clone()
+    for _ in range(3):
+        out.zero_()
+        binding.launch()
+        assert torch.equal(out, first)
+    _check_linear(oracle, m, x, first)
+
+
+def test_row_is_invariant_to_m_and_permutation():
+    n, k = 4096, 4096
+    m = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(1)) * 0.02, 4)
+    md = m.to(DEV)
+    ops = linear.PackedLinearOperators()
+    base = torch.randn((130, k), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
+    ref = ops.linear(base[:1].contiguous(), md)
+    for mrows in (3, 8, 17, 33, 65, 130):
+        y = ops.linear(base[:mrows].contiguous(), md)
+        assert torch.equal(y[:1], ref), mrows
+    perm = torch.randperm(65, generator=torch.Generator().manual_seed(3)).to(DEV)
+    y = ops.linear(base[:65].contiguous(), md)
+    yp = ops.linear(base[:65][perm].contiguous(), md)
+    assert torch.equal(yp, y[perm])
+
+
+def test_grouped_equals_separate_members():
+    k = 2048
+    gate = qz.quantize_cubic(torch.randn((768, k), generator=torch.Generator().manual_seed(7)) * 0.02, 4)
+    up = qz.quantize_cubic(torch.randn((768, k), generator=torch.Generator().manual_seed(8)) * 0.02, 4)
+    gate, up = gate.to(DEV), up.to(DEV)
+    x = torch.randn((64, k), generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(DEV)
+    ops = linear.PackedLinearOperators()
+    y0 = torch.empty((64, 768), dtype=torch.bfloat16, device=DEV)
+    y1 = torch.empty_like(y0)
+    ops.bind_linear_group(x, (gate, up), (y0, y1)).launch()
+    assert torch.equal(y0, ops.linear(x, gate))
+    assert torch.equal(y1, ops.linear(x, up))
+
+
+def test_lm_head_cfg2_shape_sampled_enclosure(oracle):
+    """Qwen3-8B lm_head 151936 x 4096 W4 at M=64: enclosure on sampled row blocks."""
+    n, k = 151936, 4096
+    g = torch.Generator(device=DEV).manual_seed(0)
+    w = torch.randn((n, k), generator=g, device=DEV) * 0.02
+    m = qz.quantize_cubic(w, bits=4, group_in=128)
+    del w
+    x = torch.randn((64, k), generator=torch.Generator(device=DEV).manual_seed(1), device=DEV).to(torch.bfloat16)
+    y = linear.PackedLinearOperators().linear(x, m)
+    torch.cuda.synchronize()
+    for start in (0, 75968, n - 256):
+        part = m.rows(start, start + 256).to("cpu")
+        _check_linear(oracle, part, x, y[:, start:start + 256])
