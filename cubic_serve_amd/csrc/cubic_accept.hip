@@ -88,6 +88,67 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane) {
     return v;
 }
 
+// Descending bitonic sort of one u64 per lane across the wave.
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v, int lane) {
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+            const uint64_t o = __shfl_xor(v, stride);
+            const bool upper = (lane & stride) != 0;
+            const bool desc = (lane & size) == 0;
+            const uint64_t hi = o > v ? o : v, lo = o > v ? v : o;
+            v = (upper == desc) ? lo : hi;
+        }
+    }
+    return v;
+}
+
+// Top `want` (<= kTop) nonzero u64 keys of entries e[q] held round-robin
+// (entry index = lane + 64 q); lane r returns the rank-r key (0 if none).
+// Any `want` lanes whose maxima are >= tau carry `want` distinct entries >= tau,
+// so tau = want-th largest lane maximum bounds the answer from below.
+template <int P>
+__device__ uint64_t wave_topk_u64(const uint64_t (&e)[P], int n_entries, int want, int lane,
+                                  uint64_t* buf) {
+    if (n_entries <= kWave) return wave_sort_desc_u64(e[0], lane);
+    uint64_t lm = 0ull;
+#pragma unroll
+    for (int q = 0; q < P; ++q) lm = e[q] > lm ? e[q] : lm;
+    const uint64_t tau = __shfl(wave_sort_desc_u64(lm, lane), want - 1);
+    int mine = 0;
+#pragma unroll
+    for (int q = 0; q < P; ++q) mine += (e[q] != 0ull && e[q] >= tau);
+    int incl = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    const int total = __shfl(incl, kWave - 1);
+    if (total <= kWave) {
+        int pos = incl - mine;
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+            if (e[q] != 0ull && e[q] >= tau) buf[pos++] = e[q];
+        wave_lds_sync();
+        const uint64_t v = lane < total ? buf[lane] : 0ull;
+        wave_lds_sync();
+        return wave_sort_desc_u64(v, lane);
+    }
+    uint64_t prev = ~0ull, my = 0ull;  // many equal keys: one rank per round
+    for (int round = 0; round < want; ++round) {
+        uint64_t best = 0ull;
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+            if (e[q] < prev && e[q] > best) best = e[q];
+        best = wave_max_u64(best);
+        if (lane == round) my = best;
+        prev = best;
+    }
+    return my;
+}
+
 // --------------------------------------------------------------------------
 // Verification of one proposal row by one wave (speculative.py:46-219).
 // Virtual lanes v = lane + 64 * s, s < SLOTS, cover BLOCK = next_pow2(TP*K).
@@ -111,12 +172,18 @@ struct VerifyRow {
 
 template <int SLOTS>
 struct VerifyScratch {
-    float score[3][SLOTS * kWave];
-    int64_t id[3][SLOTS * kWave];
-    int real[3][SLOTS * kWave];
-    float sorted_score[3][SLOTS * kWave];
-    int64_t sorted_id[3][SLOTS * kWave];
-    float qprob[SLOTS * kWave];
+    float score[SLOTS * kWave];   // rank-ordered scores of the set being selected
+    int64_t id[SLOTS * kWave];
+    int64_t q_id[SLOTS * kWave];  // selected draft candidates (for q_at_p)
+    float q_prob[SLOTS * kWave];
+};
+
+// Per-lane candidate set: virtual lane v = lane + 64 * s.
+template <int SLOTS>
+struct LaneSet {
+    float s[SLOTS];
+    int64_t i[SLOTS];
+    bool r[SLOTS];
 };
 
 template <int SLOTS>
@@ -150,7 +217,7 @@ __device__ __forceinline__ void vl_scan(float (&x)[SLOTS], int block, int lane) 
         } else {
 #pragma unroll
             for (int s = 0; s < SLOTS; ++s) {
-                const float same = __shfl(x[s], lane - d);              // lane >= d
+                const float same = __shfl(x[s], lane - d);                          // lane >= d
                 const float prev = __shfl(x[s > 0 ? s - 1 : 0], lane + kWave - d);  // lane < d
                 const int v = lane + kWave * s;
                 const float other = lane >= d ? same : prev;
@@ -174,83 +241,128 @@ __device__ __forceinline__ float vl_max(const float (&x)[SLOTS], int block) {
     return __shfl(m, 0);
 }
 
-// speculative.py:11-29 on the LDS copy of one candidate set.  Writes the
-// selected (score, id) pairs in rank order to sorted_*, returns the number of
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ float readlanef(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// speculative.py:11-29.  Output: the selected (score, id) of rank v in
+// virtual lane v (v < k), (-inf, INT64_MAX) elsewhere; returns the number of
 // real lanes.  A real lane is the first of its (score, id) pair if no earlier
 // real lane repeats it; its rank is the number of first lanes strictly ahead
-// in (score desc, id asc) order.  Duplicated pairs therefore occupy one slot,
-// exactly as the reference removes every copy when it selects the pair.
+// in (score desc, id asc) order, so a duplicated pair occupies one slot,
+// exactly as the reference removes every copy of the pair it selects.
+// Fast path: real lanes already form a strictly ordered prefix (the layout
+// candidate publication produces), where selection is the identity.
 template <int SLOTS>
-__device__ int select_topk(VerifyScratch<SLOTS>& sc, int set, int block, int k, int lane) {
-    const float* score = sc.score[set];
-    const int64_t* id = sc.id[set];
-    int* real = sc.real[set];  // 0 = not real, 1 = real repeat, 2 = real first
-    float my_s[SLOTS];
-    int64_t my_i[SLOTS];
-    bool my_r[SLOTS], first[SLOTS];
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int v = lane + kWave * s;
-        my_r[s] = v < block && real[v];
-        my_s[s] = v < block ? score[v] : 0.0f;
-        my_i[s] = v < block ? id[v] : 0;
-        first[s] = my_r[s];
-    }
+__device__ int select_set(const LaneSet<SLOTS>& in, int block, int k, int lane,
+                          VerifyScratch<SLOTS>& sc, LaneSet<SLOTS>& out) {
     int count = 0;
-    for (int j = 0; j < block; ++j) {
-        const bool rj = real[j] != 0;
-        count += rj;
-        if (!rj) continue;
-        const float sj = score[j];
-        const int64_t ij = id[j];
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s)
-            if (my_r[s] && j < lane + kWave * s && sj == my_s[s] && ij == my_i[s]) first[s] = false;
-    }
-    wave_lds_sync();
+    bool ok = true;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
         const int v = lane + kWave * s;
-        if (v < block) {
-            real[v] = my_r[s] ? (first[s] ? 2 : 1) : 0;
-            sc.sorted_score[set][v] = -__builtin_huge_valf();
-            sc.sorted_id[set][v] = kInt64Max;
+        count += __builtin_popcountll(__ballot(v < block && in.r[s]));
+        // neighbour v + 1
+        const int src = lane + 1 < kWave ? lane + 1 : 0;
+        const int ss = lane + 1 < kWave ? s : (s + 1 < SLOTS ? s + 1 : s);
+        float ns = 0.0f;
+        int64_t ni = 0;
+        bool nr = false;
+#pragma unroll
+        for (int t = 0; t < SLOTS; ++t) {
+            const float ts = __shfl(in.s[t], src);
+            const int64_t ti = __shfl(in.i[t], src);
+            const bool tr = __shfl((int)in.r[t], src) != 0;
+            if (t == ss) { ns = ts; ni = ti; nr = tr; }
+        }
+        if (v + 1 < block && !(lane + 1 >= kWave && s + 1 >= SLOTS)) {
+            const bool r0 = in.r[s];
+            if (nr && !r0) ok = false;
+            if (r0 && nr && !(in.s[s] > ns || (in.s[s] == ns && in.i[s] < ni))) ok = false;
         }
     }
-    wave_lds_sync();
+    if (__all(ok)) {
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int v = lane + kWave * s;
+            const bool take = v < block && v < k && in.r[s];
+            out.s[s] = take ? in.s[s] : -__builtin_huge_valf();
+            out.i[s] = take ? in.i[s] : kInt64Max;
+            out.r[s] = take;
+        }
+        return count;
+    }
+    // general path: first-occurrence flags, then ranks, by uniform lane walks
+    bool first[SLOTS];
     int rank[SLOTS];
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) rank[s] = 0;
-    for (int j = 0; j < block; ++j) {
-        if (real[j] != 2) continue;
-        const float sj = score[j];
-        const int64_t ij = id[j];
+    for (int s = 0; s < SLOTS; ++s) { first[s] = in.r[s]; rank[s] = 0; }
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s)
-            rank[s] += (sj > my_s[s] || (sj == my_s[s] && ij < my_i[s])) ? 1 : 0;
+    for (int sj = 0; sj < SLOTS; ++sj)
+        for (int l = 0; l < kWave; ++l) {
+            const int j = l + kWave * sj;
+            if (j >= block) break;
+            if (!__builtin_amdgcn_readlane((int)in.r[sj], l)) continue;
+            const float vs = readlanef(in.s[sj], l);
+            const int64_t vi = readlane64(in.i[sj], l);
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s)
+                if (in.r[s] && j < lane + kWave * s && vs == in.s[s] && vi == in.i[s]) first[s] = false;
+        }
+#pragma unroll
+    for (int sj = 0; sj < SLOTS; ++sj)
+        for (int l = 0; l < kWave; ++l) {
+            const int j = l + kWave * sj;
+            if (j >= block) break;
+            if (!__builtin_amdgcn_readlane((int)first[sj], l)) continue;
+            const float vs = readlanef(in.s[sj], l);
+            const int64_t vi = readlane64(in.i[sj], l);
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s)
+                rank[s] += (vs > in.s[s] || (vs == in.s[s] && vi < in.i[s])) ? 1 : 0;
+        }
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        if (v < block) { sc.score[v] = -__builtin_huge_valf(); sc.id[v] = kInt64Max; }
     }
+    wave_lds_sync();
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s)
-        if (my_r[s] && first[s] && rank[s] < k) {
-            sc.sorted_score[set][rank[s]] = my_s[s];
-            sc.sorted_id[set][rank[s]] = my_i[s];
+        if (lane + kWave * s < block && first[s] && rank[s] < k) {
+            sc.score[rank[s]] = in.s[s];
+            sc.id[rank[s]] = in.i[s];
         }
+    wave_lds_sync();
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int v = lane + kWave * s;
+        out.s[s] = v < block ? sc.score[v] : -__builtin_huge_valf();
+        out.i[s] = v < block ? sc.id[v] : kInt64Max;
+        out.r[s] = out.i[s] != kInt64Max;
+    }
     wave_lds_sync();
     return count;
 }
 
-// speculative.py:32-43 for the sorted scores of one set.
+// speculative.py:32-43 for one selected set (scores in rank order).
 template <int SLOTS>
-__device__ __forceinline__ void probabilities(const float* sorted, float temperature, int64_t top_k,
-                                              float top_p, int block, int lane, float (&out)[SLOTS],
-                                              float& mass) {
+__device__ __forceinline__ void probabilities(const float (&sorted)[SLOTS], float temperature,
+                                              int64_t top_k, float top_p, int block, int lane,
+                                              float (&out)[SLOTS], float& mass) {
     const float safe_t = temperature == 0.0f ? 1.0f : temperature;
-    float logit[SLOTS], w[SLOTS], p[SLOTS], incl[SLOTS];
+    float logit[SLOTS], w[SLOTS], p[SLOTS], incl[SLOTS], tmp[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
         const int v = lane + kWave * s;
         const bool sel = v < block && v < top_k;
-        logit[s] = sel ? sorted[v] / safe_t : -__builtin_huge_valf();
+        logit[s] = sel ? sorted[s] / safe_t : -__builtin_huge_valf();
     }
     const float mx = vl_max<SLOTS>(logit, block);
 #pragma unroll
@@ -258,10 +370,8 @@ __device__ __forceinline__ void probabilities(const float* sorted, float tempera
         const int v = lane + kWave * s;
         const bool sel = v < block && v < top_k;
         w[s] = sel ? accept_expf(logit[s] - mx) : 0.0f;
+        tmp[s] = w[s];
     }
-    float tmp[SLOTS];
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) tmp[s] = w[s];
     const float sum = vl_tree_sum<SLOTS>(tmp, block);
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) { p[s] = w[s] / sum; incl[s] = p[s]; }
@@ -282,10 +392,10 @@ template <int SLOTS>
 __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int lane, int64_t* out2) {
     const int block = r.block;
     bool lane_ok = true;
+    LaneSet<SLOTS> qset, p0set, p1set;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
         const int v = lane + kWave * s;
-        if (v >= block) continue;
         const bool cm = v < r.tp * r.k;
         const int rank = cm ? v / r.k : 0, local = cm ? v % r.k : 0;
         const bool load = r.active && cm;
@@ -308,33 +418,30 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         const bool qpad = cm && qi == -1 && qs != qs;
         const bool p0pad = cm && p0i == -1 && p0s != p0s;
         const bool p1pad = cm && p1i == -1 && p1s != p1s;
-        lane_ok = lane_ok && (!cm || qr || qpad) && (!cm || p0r || p0pad) && (!cm || p1r || p1pad);
-        sc.score[0][v] = qs; sc.id[0][v] = qi; sc.real[0][v] = qr;
-        sc.score[1][v] = p0s; sc.id[1][v] = p0i; sc.real[1][v] = p0r;
-        sc.score[2][v] = p1s; sc.id[2][v] = p1i; sc.real[2][v] = p1r;
+        if (v < block)
+            lane_ok = lane_ok && (!cm || qr || qpad) && (!cm || p0r || p0pad) && (!cm || p1r || p1pad);
+        qset.s[s] = qs; qset.i[s] = qi; qset.r[s] = v < block && qr;
+        p0set.s[s] = p0s; p0set.i[s] = p0i; p0set.r[s] = v < block && p0r;
+        p1set.s[s] = p1s; p1set.i[s] = p1i; p1set.r[s] = v < block && p1r;
     }
     const bool pairs_valid = __all(lane_ok);
-    wave_lds_sync();
-    const int qc = select_topk<SLOTS>(sc, 0, block, r.k, lane);
-    const int p0c = select_topk<SLOTS>(sc, 1, block, r.k, lane);
-    const int p1c = select_topk<SLOTS>(sc, 2, block, r.k, lane);
+    LaneSet<SLOTS> q, p0, p1;
+    const int qc = select_set<SLOTS>(qset, block, r.k, lane, sc, q);
+    const int p0c = select_set<SLOTS>(p0set, block, r.k, lane, sc, p0);
+    const int p1c = select_set<SLOTS>(p1set, block, r.k, lane, sc, p1);
 
     float qp[SLOTS], p0p[SLOTS], p1p[SLOTS], qm, p0m, p1m;
-    probabilities<SLOTS>(sc.sorted_score[0], r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
-    probabilities<SLOTS>(sc.sorted_score[1], r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
-    probabilities<SLOTS>(sc.sorted_score[2], r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
+    probabilities<SLOTS>(q.s, r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
+    probabilities<SLOTS>(p0.s, r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
+    probabilities<SLOTS>(p1.s, r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
 
-    int64_t iq[SLOTS], ip0[SLOTS], ip1[SLOTS];
     float t1[SLOTS], t2[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
         const int v = lane + kWave * s;
-        iq[s] = v < block ? sc.sorted_id[0][v] : kInt64Max;
-        ip0[s] = v < block ? sc.sorted_id[1][v] : kInt64Max;
-        ip1[s] = v < block ? sc.sorted_id[2][v] : kInt64Max;
-        t1[s] = iq[s] == r.draft ? qp[s] : 0.0f;
-        t2[s] = ip0[s] == r.draft ? p0p[s] : 0.0f;
-        if (v < block) sc.qprob[v] = qp[s];
+        t1[s] = q.i[s] == r.draft ? qp[s] : 0.0f;
+        t2[s] = p0.i[s] == r.draft ? p0p[s] : 0.0f;
+        if (v < block) { sc.q_id[v] = q.i[s]; sc.q_prob[v] = qp[s]; }
     }
     const float q_draft = vl_tree_sum<SLOTS>(t1, block);
     const float p_draft = vl_tree_sum<SLOTS>(t2, block);
@@ -344,7 +451,7 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
     const float u_accept = r.uniforms ? r.uniforms[0] : philox_uniform(key, (uint32_t)(r.ordinal * 2));
     const bool random_accepted = u_accept < ratio;
     const bool greedy = r.temperature == 0.0f;
-    const int64_t p0_top = __shfl(ip0[0], 0), p1_top = __shfl(ip1[0], 0);
+    const int64_t p0_top = __shfl(p0.i[0], 0), p1_top = __shfl(p1.i[0], 0);
     const bool greedy_accepted = r.draft == p0_top;
     const bool accepted = greedy ? greedy_accepted : random_accepted;
     wave_lds_sync();
@@ -353,10 +460,10 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) q_at_p[s] = 0.0f;
     for (int pos = 0; pos < r.k; ++pos) {
-        const int64_t qid = sc.sorted_id[0][pos];
-        const float qpr = sc.qprob[pos];
+        const int64_t qid = sc.q_id[pos];
+        const float qpr = sc.q_prob[pos];
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) q_at_p[s] = ip0[s] == qid ? qpr : q_at_p[s];
+        for (int s = 0; s < SLOTS; ++s) q_at_p[s] = p0.i[s] == qid ? qpr : q_at_p[s];
     }
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
@@ -382,8 +489,14 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         if (b1) p1_slot = kWave * s + __builtin_ctzll(b1);
         if (br) res_slot = kWave * s + __builtin_ctzll(br);
     }
-    const int64_t p1_token = p1_slot < block ? sc.sorted_id[2][p1_slot] : kInt64Max;
-    const int64_t res_token = res_slot < block ? sc.sorted_id[1][res_slot] : kInt64Max;
+    int64_t p1_token = kInt64Max, res_token = kInt64Max;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int64_t a1 = __shfl(p1.i[s], p1_slot & (kWave - 1));
+        const int64_t ar = __shfl(p0.i[s], res_slot & (kWave - 1));
+        if (p1_slot < block && p1_slot / kWave == s) p1_token = a1;
+        if (res_slot < block && res_slot / kWave == s) res_token = ar;
+    }
     const int64_t need = (greedy || r.underfilled) ? 1 : r.top_k;
     const bool valid = r.active && pairs_valid && r.rows_ok && r.temperature >= 0.0f &&
                        r.temperature < __builtin_huge_valf() && r.top_k >= 1 && r.top_k <= r.k &&
@@ -467,6 +580,7 @@ struct TileScratch {
     uint16_t cand_score[9][64];
     int64_t cand_id[9][64];
     int64_t decisions[8][2];
+    uint64_t merge[kWaves][kWave];
 };
 
 // Exact top-`kTop` composites of the lane-held elements of one wave.
@@ -620,23 +734,14 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
             if (lane == round) my = b;
             prev = b;
         }
-        if (lane < kTop) part[lane] = my;
+        if (lane < kTop) store_device(&part[lane], my);
         if (lane == 0)
-            a.partial_flags[(int64_t)row * a.tiles + tile] =
-                ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3];
+            store_device(&a.partial_flags[(int64_t)row * a.tiles + tile],
+                         ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3]);
     }
     // arrival: the last workgroup of this row group finalises it
     const int group = row / a.group_rows;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t expected = (uint32_t)(a.group_rows * a.tiles);
-        const uint32_t old = atomicAdd(&a.counters[group], 1u);
-        ts.last = old == expected - 1;
-    }
-    __syncthreads();
-    if (!ts.last) return;
-    __threadfence();
+    if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) return;
 
     // ---- finalise the group's rows: merge tiles, publish candidates -------
     const int row0 = group * a.group_rows;
@@ -644,7 +749,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         const int r = row0 + gr;
         const bool own = r < a.owned_rows;
         uint32_t bad_row = 0;
-        for (int t = lane; t < a.tiles; t += kWave) bad_row |= a.partial_flags[(int64_t)r * a.tiles + t];
+        for (int t = lane; t < a.tiles; t += kWave) bad_row |= load_device(&a.partial_flags[(int64_t)r * a.tiles + t]);
         bad_row = __any(bad_row != 0);
         // kTop global winners by (value desc, id asc) over tiles * kTop entries
         constexpr int kPer = (kMaxTiles * kTop + kWave - 1) / kWave;
@@ -654,7 +759,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
             const int i = lane + q * kWave;
             entry[q] = 0ull;
             if (i < a.tiles * kTop) {
-                const uint32_t k32 = a.partial_keys[(int64_t)r * a.tiles * kTop + i];
+                const uint32_t k32 = load_device(&a.partial_keys[(int64_t)r * a.tiles * kTop + i]);
                 if (k32 != 0u) {
                     const uint32_t t = (uint32_t)(i / kTop);
                     const uint32_t id = t * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
@@ -662,17 +767,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 }
             }
         }
-        uint64_t prev = ~0ull, my = 0ull;
         const int want = a.count < kTop ? a.count : kTop;
-        for (int round = 0; round < want; ++round) {
-            uint64_t best = 0ull;
-#pragma unroll
-            for (int q = 0; q < kPer; ++q)
-                if (entry[q] < prev && entry[q] > best) best = entry[q];
-            best = wave_max_u64(best);
-            if (lane == round) my = best;
-            prev = best;
-        }
+        const uint64_t my = wave_topk_u64<kPer>(entry, a.tiles * kTop, want, lane, ts.merge[wave]);
         const float temp = a.row_temperatures[r];
         const bool greedy_pub = temp == 0.0f;
         const int j = lane;  // capacity <= 64
@@ -700,7 +796,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
     }
     if (!FUSED) {
-        if (threadIdx.x == 0) a.counters[group] = 0u;
+        if (threadIdx.x == 0) store_device(&a.counters[group], 0u);
         return;
     }
     __syncthreads();
@@ -756,7 +852,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 a.emitted[(int64_t)c * (depth + 1) + d] = tok;
             }
         }
-        a.counters[group] = 0u;
+        store_device(&a.counters[group], 0u);
     }
 }
 

@@ -4,6 +4,7 @@
 #include <string>
 #include <cstdio>
 #include <cstdarg>
+#include <cstdlib>
 
 #include "cubic_mi355x.h"
 #include "cubic_capi_internal.h"
@@ -45,29 +46,44 @@ struct GemmPlan {
     int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
 };
 
-GemmPlan plan_gemm(int64_t n, int64_t k) {
+GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
     GemmPlan p;
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
     p.tiles_per_wave = 1;
-    for (int j : {4, 2}) {
-        if (ceil_div(p.n_tiles, 4 * j) >= 128) { p.tiles_per_wave = j; break; }
-    }
+    // Two 16-column tiles per wave once that still leaves >= 128 column
+    // blocks (halves the activation-fragment LDS reads per weight byte); four
+    // would drop to one wave per SIMD (register bound) and lose the VALU/MFMA
+    // overlap.
+    if (ceil_div(p.n_tiles, 8) >= 128) p.tiles_per_wave = 2;
+#ifdef CUBIC_TIMELINE  // instrumented build only: plan overrides for sweeps
+    if (const char* e = getenv("CUBIC_DEV_J")) p.tiles_per_wave = atoi(e);
+#endif
     p.col_blocks = (int)ceil_div(p.n_tiles, 4 * p.tiles_per_wave);
-    int split = 512 / p.col_blocks;
-    if (split < 1) split = 1;
+    // K is split until about 256 workgroups are in flight (one per CU): more
+    // partitions cost more in the exchange than they gain in parallelism.
+    const int64_t out_blocks = (int64_t)p.col_blocks * ceil_div(m, 64);
+    int split = 1;
+    while (split < 8 && out_blocks * split < 256) split *= 2;
     if (split > 8) split = 8;
     if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
+#ifdef CUBIC_TIMELINE
+    if (const char* e = getenv("CUBIC_DEV_SPLIT")) split = atoi(e);
+#endif
     p.blocks_per_split = (int)ceil_div(p.k_blocks, split);
     p.split = (int)ceil_div(p.k_blocks, p.blocks_per_split);
     return p;
 }
 
+// Split-K partials: per K partition and output block (64-row chunk x column
+// block), 4 waves x J tiles x MT m-tiles x 64 lanes float4 units.
 int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
-    const GemmPlan p = plan_gemm(n, k);
+    const GemmPlan p = plan_gemm(m, n, k);
     if (p.split == 1) return 0;
-    const int64_t counters = (int64_t)p.col_blocks * ceil_div(m, 64) * 4;
-    return align256(counters) + align256((int64_t)p.split * m * n * 4);
+    const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, 64);
+    const int64_t mt = ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1));
+    const int64_t units = 4 * p.tiles_per_wave * mt * 64;
+    return align256(blocks * 4) + align256((int64_t)p.split * blocks * units * 16);
 }
 
 int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
@@ -84,7 +100,7 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
         return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
     if (ldy0 < (n_split) || (y1 && ldy1 < n - n_split))
         return fail(CUBIC_EINVAL, "output leading dimension too small");
-    const GemmPlan p = plan_gemm(n, k);
+    const GemmPlan p = plan_gemm(m, n, k);
     const int64_t need = gemm_workspace(m, n, k);
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
     if (need && !workspace) return fail(CUBIC_EINVAL, "null workspace");
@@ -110,7 +126,7 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
     a.n_tiles = p.n_tiles;
     a.tiles_per_wave = p.tiles_per_wave;
     if (p.split > 1) {
-        const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, 64) * 4);
+        const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, 64) * 4);  // one per output block
         a.counters = (uint32_t*)workspace;
         a.partials = (float*)((char*)workspace + counters);
     }
@@ -131,6 +147,7 @@ bool plan_tiles(int rows, int width, TilePlan* out) {
     if (target > kMaxTiles) target = kMaxTiles;
     int64_t tw = ceil_div(ceil_div(width, target), kChunk) * kChunk;
     const int64_t min_tw = ceil_div(ceil_div(width, kMaxTiles), kChunk) * kChunk;
+    if (tw > (int64_t)kChunk * kMaxTileChunks) tw = (int64_t)kChunk * kMaxTileChunks;
     if (tw < min_tw) tw = min_tw;
     if (tw > (int64_t)kChunk * kMaxTileChunks) return false;
     out->tile_width = (int)tw;
@@ -174,7 +191,7 @@ int cubic_prepared_words(int64_t n, int64_t k, int bits, int group_in, int64_t* 
         return fail(CUBIC_EINVAL, "invalid prepared geometry");
     const int64_t n_tiles = ceil_div(n, 16), k_blocks = ceil_div(k, kKBlock);
     if (code_words) *code_words = n_tiles * k_blocks * 64 * bits;
-    if (meta_words) *meta_words = n_tiles * ceil_div(k, group_in) * 16 * 2;
+    if (meta_words) *meta_words = n_tiles * ceil_div(k, group_in) * 16 * (bits == 4 ? 4 : 2);
     return CUBIC_OK;
 }
 

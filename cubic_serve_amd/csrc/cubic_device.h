@@ -86,4 +86,51 @@ __device__ __forceinline__ float philox_uniform(uint32_t key, uint32_t ordinal) 
     return (float)sv * 4.6566127342e-10f;
 }
 
+// Cross-workgroup hand-off without a full cache write-back: the producer
+// writes the exchanged words with device-scope atomic stores, drains its
+// memory counters, then bumps an arrival counter; the last arrival reads the
+// words with device-scope atomic loads.  (A device-scope fence would write
+// back every dirty L2 line of the XCD instead.)
+template <typename T>
+__device__ __forceinline__ void store_device(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T load_device(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 128-bit device-scope hand-off through buffer instructions: cache policy sc1
+// makes the access coherent across the XCDs' L2s (what a device-scope atomic
+// dword access compiles to), four words per instruction.
+constexpr int kCpolDevice = 16;
+typedef unsigned u32x4_dev_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_dev_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t device_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ void store_device4(__amdgpu_buffer_rsrc_t r, int byte_offset, floatx4_dev_t v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_dev_t, v), r, byte_offset, 0, kCpolDevice);
+}
+
+__device__ __forceinline__ floatx4_dev_t load_device4(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+    return __builtin_bit_cast(floatx4_dev_t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kCpolDevice));
+}
+
+// Called by every thread after its store_device() writes; returns true in
+// every thread of the workgroup that arrives last (count = expected arrivals).
+// The caller resets the counter to zero when it is done.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's device-scope stores are performed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *lds_flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    expected - 1;
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
 }  // namespace cubic

@@ -18,10 +18,25 @@
 //
 // Every decoded weight equals bf16(decode_cubic(...)) bit for bit: levels are
 // evaluated in the reference's unfused binary32 order and rounded once.
-// FP32 accumulation runs in MFMA; K partitions (fixed by N and K only) are
-// summed in ascending order by the last workgroup of each output block.
+// FP32 accumulation runs in MFMA; K partitions (fixed by N, K and the number
+// of 64-row chunks) are summed in ascending order by the last workgroup of
+// each output block.
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
+
+#ifdef CUBIC_TIMELINE
+// Development instrumentation (never built into the shipped library): per
+// workgroup s_memrealtime stamps of the GEMM main loop.
+__device__ uint64_t g_timeline[4096][40];
+extern "C" __attribute__((visibility("default"))) int cubic_dev_timeline(uint64_t* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), sizeof(g_timeline));
+}
+#define CUBIC_STAMP(slot) \
+    do { if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 4096 && (slot) < 40) \
+        g_timeline[blockIdx.x + gridDim.x * blockIdx.y][(slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define CUBIC_STAMP(slot) do {} while (0)
+#endif
 
 namespace cubic {
 namespace {
@@ -53,6 +68,12 @@ __device__ __forceinline__ float curve_level(float t, float s, float a, float b)
     return s * (t * mid);
 }
 
+// Prepared metadata words per (column, group): bits <= 4 store the group's bf16
+// level table as v_perm byte planes (4 words at 4 bits, 2 words below);
+// bits >= 5 store (scale f32, a f16 | b f16 << 16).
+template <int BITS>
+__host__ __device__ constexpr int meta_words() { return BITS == 4 ? 4 : 2; }
+
 // ---------------------------------------------------------------------------
 // Level tables for bits <= 4: magnitudes 0..7 -> bf16, split into low-byte and
 // high-byte planes so one v_perm_b32 looks up four magnitudes.
@@ -76,16 +97,6 @@ __device__ __forceinline__ uint32_t level_pair(int m0, float s, float a, float b
     return pack_bf16x2(l0, l1);
 }
 
-template <int BITS>
-__device__ __forceinline__ uint32_t level_pair_dyn(int q, float s, float a, float b) {
-    // q in 0..3 selects the pair (2q, 2q + 1); unrolled so t stays a constant
-    uint32_t r = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (i == q) r = level_pair<BITS>(2 * i, s, a, b);
-    return r;
-}
-
 __device__ __forceinline__ LevelTable table_from_pairs(uint32_t p0, uint32_t p1, uint32_t p2,
                                                        uint32_t p3) {
     LevelTable t;
@@ -94,28 +105,6 @@ __device__ __forceinline__ LevelTable table_from_pairs(uint32_t p0, uint32_t p1,
     t.lo_hi = perm(p3, p2, 0x06040200u);
     t.hi_hi = perm(p3, p2, 0x07050301u);
     return t;
-}
-
-// Table for this lane's (column, group).  When a group spans the whole
-// 128-k block the four lanes sharing it (l, l^16, l^32, l^48) each evaluate
-// one level pair and exchange them; otherwise the lane evaluates all pairs.
-template <int BITS>
-__device__ __forceinline__ LevelTable make_table(float s, float a, float b, int lane, bool shared) {
-    if (shared) {
-        const int q = lane >> 4;
-        const uint32_t mine = level_pair_dyn<BITS>(q, s, a, b);
-        const int base = lane & 15;
-        const uint32_t p0 = __shfl(mine, base);
-        const uint32_t p1 = __shfl(mine, base + 16);
-        const uint32_t p2 = __shfl(mine, base + 32);
-        const uint32_t p3 = __shfl(mine, base + 48);
-        return table_from_pairs(p0, p1, p2, p3);
-    }
-    const uint32_t p0 = level_pair<BITS>(0, s, a, b);
-    const uint32_t p1 = BITS >= 3 ? level_pair<BITS>(2, s, a, b) : 0u;
-    const uint32_t p2 = BITS >= 4 ? level_pair<BITS>(4, s, a, b) : 0u;
-    const uint32_t p3 = BITS >= 4 ? level_pair<BITS>(6, s, a, b) : 0u;
-    return table_from_pairs(p0, p1, p2, p3);
 }
 
 // Four bf16 pairs (k = 8f .. 8f+7) from magnitude selectors and sign bytes.
@@ -195,9 +184,76 @@ __device__ __forceinline__ uint4 direct_fragment(const uint32_t* w, int f, float
 //   grid.y: K partitions (split)
 //   grid.z: 64-row chunks of M
 // ---------------------------------------------------------------------------
-template <int BITS, int MT, int J>
+// Code words of one lane for one (tile, k-block): vector loads, streamed once.
+template <int W>
+__device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&dst)[W]) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    if constexpr (W == 4) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    } else if constexpr (W == 2) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+        dst[0] = v.x; dst[1] = v.y;
+    } else if constexpr (W == 8) {
+        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+        const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + 1);
+        dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
+        dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+    } else {
+#pragma unroll
+        for (int w = 0; w < W; ++w) dst[w] = __builtin_nontemporal_load(src + w);
+    }
+}
+
+// Prefetch depth (k-blocks of codes in flight per wave) by code words per tile.
+template <int BITS, int J>
+struct Stages {  // even (the activation stages alternate within the unrolled ring)
+    static constexpr int value = (J * BITS <= 4) ? 8 : (J * BITS <= 8 ? 6 : (J * BITS <= 16 ? 4 : 2));
+};
+
+// Last arrival of a split-K output block: sums the S partitions of each unit
+// in ascending K order and stores bf16.  Every partition load of a batch of
+// units is in flight at once (the exchange is latency bound, not bandwidth
+// bound); thread t owns units t, t + 256, ...
+template <int S, int J, int MT>
+__device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buffer_rsrc_t part,
+                                                int split_bytes, int m0) {
+    constexpr int kPer = J * MT;  // units per thread
+    constexpr int kBatch = kPer < 4 ? kPer : 4;
+#pragma unroll 1
+    for (int b0 = 0; b0 < kPer; b0 += kBatch) {
+        floatx4_dev_t v[kBatch][S];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (int sp = 0; sp < S; ++sp)
+                v[b][sp] = load_device4(part, sp * split_bytes + ((b0 + b) * kThreads + threadIdx.x) * 16);
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            floatx4_dev_t sum = v[b][0];
+#pragma unroll
+            for (int sp = 1; sp < S; ++sp) sum += v[b][sp];
+            const int u = (b0 + b) * kThreads + threadIdx.x;
+            const int uw = u / (J * MT * kWave), uj = (u / (MT * kWave)) % J;
+            const int umt = (u / kWave) % MT, ul = u % kWave;
+            const int n = ((blockIdx.x * 4 + uw) * J + uj) * 16 + (ul & 15);
+            if (n >= a.n) continue;
+            uint16_t* y = n < a.n_split ? a.y0 + n : a.y1 + (n - a.n_split);
+            const int64_t ldy = n < a.n_split ? a.ldy0 : a.ldy1;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + umt * 16 + 4 * (ul >> 4) + r;
+                if (m < a.m) y[(int64_t)m * ldy] = (uint16_t)float_to_bf16_bits(sum[r]);
+            }
+        }
+    }
+}
+
+template <int BITS, int MT, int J, bool G128>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
+    constexpr int S = Stages<BITS, J>::value;
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][64 * kALd];
     __shared__ float t_lds[128];
 
@@ -212,6 +268,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
     if constexpr (BITS >= 5) {
         for (int i = threadIdx.x; i < (1 << (BITS - 1)); i += kThreads)
             t_lds[i] = (float)((double)i / (double)((1 << (BITS - 1)) - 1));
+        __syncthreads();
     }
 
     floatx4_t acc[MT][J];
@@ -220,112 +277,150 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < J; ++j) acc[mt][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    // --- per-k-block loads -------------------------------------------------
-    uint32_t nxt_codes[J][W];
-    uint32_t nxt_meta[J][2];
-    uint4 nxt_a[4];
-    auto load_block = [&](int kb) {
+    // --- code/metadata ring: stage s holds k-block kb with kb % S == s -------
+    // Loads are unconditional: a tile past N or a k-block past this split reads
+    // a clamped in-bounds address and its result is never consumed or stored.
+    const uint32_t* code_base[J];
+    const uint32_t* meta_base[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int nt = min(tile0 + j, a.n_tiles - 1);
+        code_base[j] = a.codes + ((int64_t)nt * a.k_blocks * kWave + lane) * W;
+        meta_base[j] = a.meta + ((int64_t)nt * a.groups_k * 16 + col) * meta_words<BITS>();
+    }
+    const int gq = G128 ? 0 : 32 * q;  // G128: group_in is a multiple of 128
+    uint32_t ring_codes[S][J][W];
+    constexpr int MW = meta_words<BITS>();
+    uint32_t ring_meta[S][J][MW];
+    auto load_codes = [&](int kb, uint32_t (&codes)[J][W], uint32_t (&meta)[J][MW]) {
+        kb = min(kb, kb_end - 1);
+        const int g = (kb * kKBlock + gq) / a.group_in;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int nt = tile0 + j;
-            if (nt < a.n_tiles) {
-                const uint32_t* src = a.codes + (((int64_t)nt * a.k_blocks + kb) * kWave + lane) * W;
-#pragma unroll
-                for (int w = 0; w < W; ++w) nxt_codes[j][w] = src[w];
-                const int g = (kb * kKBlock + 32 * q) / a.group_in;
-                const uint32_t* ms = a.meta + (((int64_t)nt * a.groups_k + g) * 16 + col) * 2;
-                nxt_meta[j][0] = ms[0];
-                nxt_meta[j][1] = ms[1];
+            load_words<W>(code_base[j] + kb * (kWave * W), codes[j]);
+            const uint32_t* mp = meta_base[j] + g * (16 * MW);
+            if constexpr (MW == 4) {
+                const uint4 mv = *reinterpret_cast<const uint4*>(mp);
+                meta[j][0] = mv.x; meta[j][1] = mv.y; meta[j][2] = mv.z; meta[j][3] = mv.w;
             } else {
-#pragma unroll
-                for (int w = 0; w < W; ++w) nxt_codes[j][w] = 0u;
-                nxt_meta[j][0] = nxt_meta[j][1] = 0u;
+                const uint2 mv = *reinterpret_cast<const uint2*>(mp);
+                meta[j][0] = mv.x; meta[j][1] = mv.y;
             }
         }
-        // activations: 64 rows x 128 k = 1024 chunks of 8 bf16, 4 per thread
+    };
+    // activations: 64 rows x 128 k = 1024 chunks of 8 bf16, 4 per thread.
+    // k % 8 == 0 (admission): a chunk is wholly inside or outside K; rows past
+    // M read row M-1 (their outputs are discarded), chunks past K are zero.
+    // Two register stages: the block for kb + 2 is in flight while kb is used.
+    uint4 act[2][4];
+    const uint16_t* act_row[4];
+    int act_c8[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int chunk = threadIdx.x + kThreads * i;
-            const int r = chunk >> 4, c8 = (chunk & 15) * 8;
-            const int m = m0 + r, k = kb * kKBlock + c8;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (r < MT * 16 && m < a.m) {
-                const uint16_t* src = a.x + (int64_t)m * a.ldx + k;
-                if (k + 8 <= a.k) {
-                    v = *reinterpret_cast<const uint4*>(src);
-                } else if (k < a.k) {
-                    uint32_t wv[4] = {0, 0, 0, 0};
-                    for (int e = 0; e < 8; ++e)
-                        if (k + e < a.k) wv[e >> 1] |= (uint32_t)src[e] << ((e & 1) * 16);
-                    v = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-                }
-            }
-            nxt_a[i] = v;
+    for (int i = 0; i < 4; ++i) {
+        const int chunk = threadIdx.x + kThreads * i;
+        const int r = chunk >> 4;
+        act_c8[i] = (chunk & 15) * 8;
+        act_row[i] = a.x + (int64_t)min(m0 + r, a.m - 1) * a.ldx + act_c8[i];
+    }
+    // rows 16*MT.. are not needed: chunk i covers rows 16i..16i+15, so only i < MT
+    auto load_act = [&](int kb, uint4 (&dst)[4]) {
+        const int kofs = min(kb, kb_end - 1) * kKBlock;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const bool inside = kofs + act_c8[i] < a.k;
+            const uint32_t keep = inside ? 0xFFFFFFFFu : 0u;  // arithmetic mask: no branch
+            const uint4 v = *reinterpret_cast<const uint4*>(act_row[i] + (inside ? kofs : 0));
+            dst[i] = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
         }
     };
 
-    if (kb_begin < kb_end) load_block(kb_begin);
-    const bool shared_groups = (a.group_in % kKBlock) == 0;
-    int buf = 0;
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
-        // publish this block's activations, take its codes/metadata
+    // Issue order matters: vector-memory loads complete in order, so each
+    // iteration issues the activation block it will need two iterations later
+    // before the code block it will need S iterations later; waiting for an
+    // activation block then never drains the deeper code ring.
+    CUBIC_STAMP(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int chunk = threadIdx.x + kThreads * i;
-            const int r = chunk >> 4, c8 = (chunk & 15) * 8;
-            if (r < MT * 16)
-                *reinterpret_cast<uint4*>(&a_lds[buf][r * kALd + c8]) = nxt_a[i];
-        }
-        uint32_t codes[J][W];
-        uint32_t meta[J][2];
+    for (int st = 0; st < S; ++st) load_codes(kb_begin + st, ring_codes[st], ring_meta[st]);
+    load_act(kb_begin, act[0]);
+    load_act(kb_begin + 1, act[1]);
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += S) {
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
+        for (int st = 0; st < S; ++st) {
+            const int kb = kb0 + st;
+            if (kb >= kb_end) break;
+            constexpr int kStageMask = 1;
+            const int ab = st & kStageMask;  // S is even: the stage alternates every block
+            uint16_t* lds = a_lds[ab];
 #pragma unroll
-            for (int w = 0; w < W; ++w) codes[j][w] = nxt_codes[j][w];
-            meta[j][0] = nxt_meta[j][0];
-            meta[j][1] = nxt_meta[j][1];
-        }
-        __syncthreads();
-        if (kb + 1 < kb_end) load_block(kb + 1);
-
-        // level tables for this block
-        LevelTable tab[J];
-        float ms[J], ma[J], mb[J];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            ms[j] = __uint_as_float(meta[j][0]);
-            ma[j] = half_bits_to_float(meta[j][1] & 0xFFFFu);
-            mb[j] = half_bits_to_float(meta[j][1] >> 16);
-            if constexpr (BITS <= 4) tab[j] = make_table<BITS>(ms[j], ma[j], mb[j], lane, shared_groups);
-        }
-
-        const uint16_t* abase = &a_lds[buf][col * kALd + 32 * q];
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            bf16x8_t afrag[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const uint4 v = *reinterpret_cast<const uint4*>(abase + mt * 16 * kALd + 8 * f);
-                afrag[mt] = __builtin_bit_cast(bf16x8_t, v);
+            for (int i = 0; i < MT; ++i) {
+                const int r = (threadIdx.x >> 4) + 16 * i;
+                *reinterpret_cast<uint4*>(&lds[r * kALd + act_c8[i]]) = act[ab][i];
             }
+            uint32_t codes[J][W];
+            uint32_t meta[J][MW];
 #pragma unroll
             for (int j = 0; j < J; ++j) {
-                uint4 bw;
-                if constexpr (BITS <= 4)
-                    bw = decode_fragment<BITS>(codes[j], f, tab[j]);
-                else
-                    bw = direct_fragment<BITS>(codes[j], f, ms[j], ma[j], mb[j], t_lds);
-                const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[mt], bfrag,
-                                                                         acc[mt][j], 0, 0, 0);
+                for (int w = 0; w < W; ++w) codes[j][w] = ring_codes[st][j][w];
+#pragma unroll
+                for (int w = 0; w < MW; ++w) meta[j][w] = ring_meta[st][j][w];
             }
+            // LDS hand-off only: no vector-memory drain at the barrier
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            CUBIC_STAMP(1 + kb - kb_begin);
+            load_act(kb + 2, act[ab]);
+            load_codes(kb + S, ring_codes[st], ring_meta[st]);
+
+            // level tables (bits <= 4, prepared) or curve parameters (bits >= 5)
+            LevelTable tab[J];
+            float ms[J], ma[J], mb[J];
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                if constexpr (BITS <= 4) {
+                    tab[j].lo_lo = meta[j][0];
+                    tab[j].hi_lo = meta[j][1];
+                    tab[j].lo_hi = MW == 4 ? meta[j][MW == 4 ? 2 : 0] : 0u;
+                    tab[j].hi_hi = MW == 4 ? meta[j][MW == 4 ? 3 : 1] : 0u;
+                    ms[j] = ma[j] = mb[j] = 0.0f;
+                } else {
+                    ms[j] = __uint_as_float(meta[j][0]);
+                    ma[j] = half_bits_to_float(meta[j][1] & 0xFFFFu);
+                    mb[j] = half_bits_to_float(meta[j][1] >> 16);
+                }
+            }
+
+            const uint16_t* abase = &lds[col * kALd + 32 * q];
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                bf16x8_t afrag[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(abase + mt * 16 * kALd + 8 * f);
+                    afrag[mt] = __builtin_bit_cast(bf16x8_t, v);
+                }
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    uint4 bw;
+                    if constexpr (BITS <= 4)
+                        bw = decode_fragment<BITS>(codes[j], f, tab[j]);
+                    else
+                        bw = direct_fragment<BITS>(codes[j], f, ms[j], ma[j], mb[j], t_lds);
+                    const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[mt], bfrag,
+                                                                             acc[mt][j], 0, 0, 0);
+                }
+            }
+            // every wave finished reading this LDS stage before it is rewritten
+            // two blocks later (the next barrier orders it)
+            __builtin_amdgcn_s_waitcnt(0xC07F);
         }
-        buf ^= 1;
     }
 
     // --- epilogue -----------------------------------------------------------
+    CUBIC_STAMP(34);
     if (a.split == 1) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
@@ -343,63 +438,72 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
         }
         return;
     }
-    // split-K: FP32 partials [split][m][n], then the last arrival sums them in order
-    float* part = a.partials + (int64_t)split * a.m * a.n;
+    // split-K: each workgroup stores its FP32 accumulators in the MFMA-native
+    // layout (one 16-byte unit per tile, m-tile and lane); the last arrival
+    // sums the K partitions in ascending order.
+    constexpr int kUnits = 4 * J * MT * kWave;  // float4 units per output block
+    const int block = blockIdx.z * gridDim.x + blockIdx.x;
+    const int split_bytes = (int)(gridDim.x * gridDim.z) * kUnits * 16;  // < 2^31: split > 1 only below 256 blocks of <= 64 KiB
+    const __amdgpu_buffer_rsrc_t part =
+        device_rsrc(reinterpret_cast<char*>(a.partials) + (int64_t)block * kUnits * 16);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int n = (tile0 + j) * 16 + col;
-        if (n >= a.n) continue;
+    for (int j = 0; j < J; ++j)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + mt * 16 + 4 * q + r;
-                if (m < a.m) part[(int64_t)m * a.n + n] = acc[mt][j][r];
-            }
-    }
+            store_device4(part, split * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
+                          acc[mt][j]);
     __shared__ uint32_t last;
-    __threadfence();
-    __syncthreads();
-    const int counter = blockIdx.z * gridDim.x + blockIdx.x;
-    if (threadIdx.x == 0) last = atomicAdd(&a.counters[counter], 1u) == (uint32_t)(a.split - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const int cols = 4 * J * 16, rows = MT * 16;
-    const int n0 = blockIdx.x * cols;
-    for (int e = threadIdx.x; e < rows * cols; e += kThreads) {
-        const int m = m0 + e / cols, n = n0 + e % cols;
-        if (m >= a.m || n >= a.n) continue;
-        const int64_t off = (int64_t)m * a.n + n;
-        float sum = a.partials[off];
-        for (int sp = 1; sp < a.split; ++sp) sum = sum + a.partials[(int64_t)sp * a.m * a.n + off];
-        const uint16_t bits = (uint16_t)float_to_bf16_bits(sum);
-        if (n < a.n_split) a.y0[(int64_t)m * a.ldy0 + n] = bits;
-        else a.y1[(int64_t)m * a.ldy1 + (n - a.n_split)] = bits;
+    CUBIC_STAMP(35);
+    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) { CUBIC_STAMP(36); return; }
+    CUBIC_STAMP(37);
+    switch (a.split) {
+        case 2: reduce_partials<2, J, MT>(a, part, split_bytes, m0); break;
+        case 3: reduce_partials<3, J, MT>(a, part, split_bytes, m0); break;
+        case 4: reduce_partials<4, J, MT>(a, part, split_bytes, m0); break;
+        case 5: reduce_partials<5, J, MT>(a, part, split_bytes, m0); break;
+        case 6: reduce_partials<6, J, MT>(a, part, split_bytes, m0); break;
+        case 7: reduce_partials<7, J, MT>(a, part, split_bytes, m0); break;
+        default: reduce_partials<8, J, MT>(a, part, split_bytes, m0); break;
     }
-    if (threadIdx.x == 0) a.counters[counter] = 0u;
+    CUBIC_STAMP(38);
+    if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
 }
 
 // ---------------------------------------------------------------------------
 // Load-time preparation
 // ---------------------------------------------------------------------------
-// Metadata: per (column, group) words (scale, a | b << 16); padding columns 0.
+// Metadata: per (column, group) words; padding columns are zero.  bits <= 4:
+// the group's level table as byte planes (lo bytes of L0..3, hi bytes of L0..3,
+// lo bytes of L4..7, hi bytes of L4..7), each level bf16(curve) evaluated in
+// the reference's operation order; bits >= 5: (scale, a | b << 16).
+template <int BITS>
 __global__ void prepare_meta_kernel(const float* scale, const uint16_t* av, const uint16_t* bv,
                                     int64_t n, int groups_k, int n_tiles, uint32_t* meta) {
+    constexpr int MW = meta_words<BITS>();
     const int64_t total = (int64_t)n_tiles * groups_k * 16;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int c = (int)(i % 16);
         const int64_t g = (i / 16) % groups_k, nt = i / (16 * (int64_t)groups_k);
         const int64_t row = nt * 16 + c;
-        uint32_t w0 = 0, w1 = 0;
+        uint32_t w[4] = {0, 0, 0, 0};
         if (row < n) {
             const int64_t src = row * groups_k + g;
-            w0 = __float_as_uint(scale[src]);
-            w1 = (uint32_t)av[src] | ((uint32_t)bv[src] << 16);
+            if constexpr (BITS <= 4) {
+                const float sc = scale[src], a = half_bits_to_float(av[src]), b = half_bits_to_float(bv[src]);
+                const uint32_t p0 = level_pair<BITS>(0, sc, a, b);
+                const uint32_t p1 = BITS >= 3 ? level_pair<BITS>(2, sc, a, b) : 0u;
+                const uint32_t p2 = BITS >= 4 ? level_pair<BITS>(4, sc, a, b) : 0u;
+                const uint32_t p3 = BITS >= 4 ? level_pair<BITS>(6, sc, a, b) : 0u;
+                const LevelTable t = table_from_pairs(p0, p1, p2, p3);
+                w[0] = t.lo_lo; w[1] = t.hi_lo; w[2] = t.lo_hi; w[3] = t.hi_hi;
+            } else {
+                w[0] = __float_as_uint(scale[src]);
+                w[1] = (uint32_t)av[src] | ((uint32_t)bv[src] << 16);
+            }
         }
-        meta[2 * i] = w0;
-        meta[2 * i + 1] = w1;
+#pragma unroll
+        for (int x = 0; x < MW; ++x) meta[MW * i + x] = w[x];
     }
 }
 
@@ -533,12 +637,20 @@ __global__ void expand_metadata_kernel(int fmt, const void* m0, const void* m1, 
     }
 }
 
+template <int BITS, int MT, bool G128>
+hipError_t launch_g(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
+#ifdef CUBIC_TIMELINE
+    if (j == 4) { gemm_kernel<BITS, MT, 4, G128><<<grid, kThreads, 0, s>>>(a); return hipGetLastError(); }
+#endif
+    if (j == 2) gemm_kernel<BITS, MT, 2, G128><<<grid, kThreads, 0, s>>>(a);
+    else gemm_kernel<BITS, MT, 1, G128><<<grid, kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 template <int BITS, int MT>
 hipError_t launch_j(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
-    if (j == 4) gemm_kernel<BITS, MT, 4><<<grid, kThreads, 0, s>>>(a);
-    else if (j == 2) gemm_kernel<BITS, MT, 2><<<grid, kThreads, 0, s>>>(a);
-    else gemm_kernel<BITS, MT, 1><<<grid, kThreads, 0, s>>>(a);
-    return hipGetLastError();
+    if (a.group_in % kKBlock == 0) return launch_g<BITS, MT, true>(a, j, grid, s);
+    return launch_g<BITS, MT, false>(a, j, grid, s);
 }
 
 template <int BITS>
@@ -551,7 +663,8 @@ hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t 
 }  // namespace
 
 // MT (16-row tiles per 64-row chunk) follows m; J and the K split come from the
-// host plan, which depends on (n, k) only so results are invariant to m.
+// host plan: J from n, the K split from the number of output blocks (so a
+// row's result is the same for every m up to one 64-row chunk).
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     const int mt = a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1);
     const int rows_chunks = (a.m + 63) / 64;
@@ -592,7 +705,12 @@ hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t
     if (e != hipSuccess) return e;
     const int64_t meta_threads = (int64_t)n_tiles * groups_k * 16;
     const int mblocks = (int)((meta_threads + 255) / 256 < 65535 ? (meta_threads + 255) / 256 : 65535);
-    prepare_meta_kernel<<<mblocks, 256, 0, s>>>(scale, av, bv, n, groups_k, n_tiles, meta);
+    switch (bits) {
+#define CUBIC_META(B) case B: prepare_meta_kernel<B><<<mblocks, 256, 0, s>>>(scale, av, bv, n, groups_k, n_tiles, meta); break;
+        CUBIC_META(1) CUBIC_META(2) CUBIC_META(3) CUBIC_META(4)
+        CUBIC_META(5) CUBIC_META(6) CUBIC_META(7) CUBIC_META(8)
+#undef CUBIC_META
+    }
     return hipGetLastError();
 }
 

@@ -32,7 +32,7 @@ def test_host_planning_entry_points():
     _native.call("cubic_prepared_words", 151936, 4096, 4, 128, _native.ctypes.byref(cw),
                  _native.ctypes.byref(mw))
     assert cw.value * 4 == 151936 * 4096 * 4 // 8       # 4-bit codes, no padding
-    assert mw.value * 4 == 151936 * (4096 // 128) * 8   # 8 bytes per group
+    assert mw.value * 4 == 151936 * (4096 // 128) * 16  # prepared 4-bit level table per group
     assert lib.cubic_gemm_workspace_bytes(64, 151936, 4096, 4) == 0   # no K split for the lm_head
     assert lib.cubic_gemm_workspace_bytes(64, 4096, 12288, 4) > 0     # down projection splits K
     assert lib.cubic_gemm_workspace_bytes(1, 4096, 12288, 4) < lib.cubic_gemm_workspace_bytes(64, 4096, 12288, 4)

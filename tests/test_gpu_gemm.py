@@ -138,19 +138,23 @@ def test_split_k_path_enclosure_and_repeatability(oracle):
 
 
 def test_row_is_invariant_to_m_and_permutation():
+    # Up to 64 rows (one row chunk: the verify regime) the launch plan, and so
+    # each row's summation order, does not depend on M; beyond that the K split
+    # shrinks with M, so invariance is checked under permutation at fixed M.
     n, k = 4096, 4096
     m = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(1)) * 0.02, 4)
     md = m.to(DEV)
     ops = linear.PackedLinearOperators()
     base = torch.randn((130, k), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
     ref = ops.linear(base[:1].contiguous(), md)
-    for mrows in (3, 8, 17, 33, 65, 130):
+    for mrows in (3, 8, 17, 33, 64):
         y = ops.linear(base[:mrows].contiguous(), md)
         assert torch.equal(y[:1], ref), mrows
-    perm = torch.randperm(65, generator=torch.Generator().manual_seed(3)).to(DEV)
-    y = ops.linear(base[:65].contiguous(), md)
-    yp = ops.linear(base[:65][perm].contiguous(), md)
-    assert torch.equal(yp, y[perm])
+    for mrows in (64, 65, 130):
+        perm = torch.randperm(mrows, generator=torch.Generator().manual_seed(3)).to(DEV)
+        y = ops.linear(base[:mrows].contiguous(), md)
+        yp = ops.linear(base[:mrows][perm].contiguous(), md)
+        assert torch.equal(yp, y[perm]), mrows
 
 
 def test_grouped_equals_separate_members():
