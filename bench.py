@@ -54,7 +54,13 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-rows", type=int, default=6144,
                     help="lm_head rows in the CPU-baseline sample")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                                      "profiles", "gemm_lm_head_cfg2_traffic.json"))
+                                                      "profiles", "gemm_lm_head_cfg2_traffic.md"),
+                    help="measured HBM bytes per lm_head launch (line 'hbm_bytes_per_launch: N')")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="profiling aid: launch only the lm_head GEMM, eagerly, --steps times")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="profiling aid: run --steps elementwise negations over this many bytes "
+                         "(reads and writes each byte once; scales the HBM traffic counters)")
     return ap.parse_args(argv)
 
 
@@ -158,6 +164,24 @@ def time_graph(graph, reps: int, warmup: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def time_eager(fn, reps: int, warmup: int) -> float:
+    """Average ms per launch of back-to-back launches, HIP events recorded on
+    the stream the launches go to (torch's current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
 def cpu_baseline(step: dict, rows: int) -> dict:
     """CPU oracle (scalar C, 1 thread) on a bounded sample of the same step:
     decode + bf16 round + FP32 dot for lm_head rows [0, rows) at M = 64, and
@@ -200,7 +224,19 @@ def main(argv=None) -> int:
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 2, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        return 0
     step = build_step(args.layers)
+    if args.kernel_only:
+        for _ in range(args.steps):
+            step["lm_binding"].launch()
+        torch.cuda.synchronize()
+        return 0
 
     def run_step():
         for b in step["layer_bindings"]:
@@ -229,8 +265,7 @@ def main(argv=None) -> int:
     ms_per_step = start.elapsed_time(end) / args.steps
 
     # component breakdown and the dominant kernel's launch duration
-    lm_graph = capture(lambda: step["lm_binding"].launch())
-    lm_ms = time_graph(lm_graph, 50, 5)
+    lm_ms = time_eager(step["lm_binding"].launch, 50, 5)
     acc_graph = capture(lambda: step["plan"].launch())
     acc_ms = time_graph(acc_graph, 200, 10)
 
@@ -240,7 +275,9 @@ def main(argv=None) -> int:
     traffic = None
     if os.path.exists(args.traffic):
         with open(args.traffic) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(line.split(":", 1)[1])
     result = {
         "metric": "verify-step µs + Cubic-GEMM HBM GB/s (% peak), Qwen3-8B-shaped W4, M=64",
         "value": round(value, 2),

@@ -44,7 +44,14 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
 constexpr int kKBlock = 128;
-constexpr int kALd = kKBlock + 8;  // LDS row pitch in bf16 (16-byte pad: conflict-free b128 reads)
+// Activation stage in LDS: per 16-row block, 16-byte chunk c (k = 8c..8c+7 of
+// the k-block) of row r sits in 16-byte slot c * 16 + (r ^ c).  An MFMA
+// A-fragment read (16 rows of one chunk per 16 lanes) and a row-contiguous
+// write (16 chunks of one row per 16 lanes) then each touch 16 distinct slots
+// of one 256-byte line: measured ~1.6x the read throughput of a padded
+// row-major tile on gfx950.
+constexpr int kAStage = 64 * kKBlock;  // bf16 per stage (64 rows)
+__device__ __forceinline__ int a_slot(int r16, int c) { return c * 16 + (r16 ^ c); }
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float floatx4_t;
@@ -208,8 +215,8 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&dst)[
 
 // Prefetch depth (k-blocks of codes in flight per wave) by code words per tile.
 template <int BITS, int J>
-struct Stages {  // even (the activation stages alternate within the unrolled ring)
-    static constexpr int value = (J * BITS <= 4) ? 8 : (J * BITS <= 8 ? 6 : (J * BITS <= 16 ? 4 : 2));
+struct Stages {  // a power of two: divides the usual per-split k-block counts
+    static constexpr int value = (J * BITS <= 4) ? 8 : (J * BITS <= 16 ? 4 : 2);
 };
 
 // Last arrival of a split-K output block: sums the S partitions of each unit
@@ -254,7 +261,7 @@ template <int BITS, int MT, int J, bool G128>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
     constexpr int S = Stages<BITS, J>::value;
-    __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][64 * kALd];
+    __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
     __shared__ float t_lds[128];
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -323,38 +330,40 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
         act_row[i] = a.x + (int64_t)min(m0 + r, a.m - 1) * a.ldx + act_c8[i];
     }
     // rows 16*MT.. are not needed: chunk i covers rows 16i..16i+15, so only i < MT
+    // The loaded registers are carried unmodified (any use right after the
+    // load would make the wave wait for it); chunks past K read chunk 0 and
+    // are zeroed when written to LDS.
     auto load_act = [&](int kb, uint4 (&dst)[4]) {
         const int kofs = min(kb, kb_end - 1) * kKBlock;
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            const bool inside = kofs + act_c8[i] < a.k;
-            const uint32_t keep = inside ? 0xFFFFFFFFu : 0u;  // arithmetic mask: no branch
-            const uint4 v = *reinterpret_cast<const uint4*>(act_row[i] + (inside ? kofs : 0));
-            dst[i] = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
-        }
+        for (int i = 0; i < MT; ++i)
+            dst[i] = *reinterpret_cast<const uint4*>(act_row[i] + (kofs + act_c8[i] < a.k ? kofs : 0));
     };
 
-    // Issue order matters: vector-memory loads complete in order, so each
-    // iteration issues the activation block it will need two iterations later
-    // before the code block it will need S iterations later; waiting for an
-    // activation block then never drains the deeper code ring.
     CUBIC_STAMP(0);
 #pragma unroll
     for (int st = 0; st < S; ++st) load_codes(kb_begin + st, ring_codes[st], ring_meta[st]);
     load_act(kb_begin, act[0]);
     load_act(kb_begin + 1, act[1]);
+    // Whole groups of S k-blocks, with no exit inside the unrolled group (an
+    // exit there makes the wait-count analysis drain the ring at the loop
+    // edge).  Blocks past the split's end read clamped addresses and get zero
+    // activations, so they add exactly 0 to the accumulators.
     for (int kb0 = kb_begin; kb0 < kb_end; kb0 += S) {
 #pragma unroll
         for (int st = 0; st < S; ++st) {
             const int kb = kb0 + st;
-            if (kb >= kb_end) break;
             constexpr int kStageMask = 1;
             const int ab = st & kStageMask;  // S is even: the stage alternates every block
             uint16_t* lds = a_lds[ab];
+            const uint32_t keep =  // same for all i
+                kb < kb_end && kb * kKBlock + act_c8[0] < a.k ? 0xFFFFFFFFu : 0u;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
                 const int r = (threadIdx.x >> 4) + 16 * i;
-                *reinterpret_cast<uint4*>(&lds[r * kALd + act_c8[i]]) = act[ab][i];
+                const uint4 v = act[ab][i];
+                *reinterpret_cast<uint4*>(&lds[(i * 256 + a_slot(r & 15, act_c8[i] >> 3)) * 8]) =
+                    make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
             }
             uint32_t codes[J][W];
             uint32_t meta[J][MW];
@@ -370,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
             __builtin_amdgcn_s_barrier();
             CUBIC_STAMP(1 + kb - kb_begin);
             load_act(kb + 2, act[ab]);
-            load_codes(kb + S, ring_codes[st], ring_meta[st]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the prefetch where it is issued
 
             // level tables (bits <= 4, prepared) or curve parameters (bits >= 5)
             LevelTable tab[J];
@@ -390,14 +399,23 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
                 }
             }
 
-            const uint16_t* abase = &lds[col * kALd + 32 * q];
+            // fragment f of lane (col, q): chunk 4q + f of row col in each 16-row block
+            auto afrag_at = [&](int mt, int f) {
+                return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                        &lds[(mt * 256 + a_slot(col, 4 * q + f)) * 8]));
+            };
+            // A fragments are double-buffered: the LDS reads of fragment f + 1
+            // are in flight while fragment f is decoded and multiplied.
+            // A fragments are double-buffered: the LDS reads of fragment f + 1
+            // are in flight while fragment f is decoded and multiplied.
+            bf16x8_t afrag_buf[2][MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) afrag_buf[0][mt] = afrag_at(mt, 0);
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
-                bf16x8_t afrag[MT];
+                if (f + 1 < 4) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(abase + mt * 16 * kALd + 8 * f);
-                    afrag[mt] = __builtin_bit_cast(bf16x8_t, v);
+                    for (int mt = 0; mt < MT; ++mt) afrag_buf[(f + 1) & 1][mt] = afrag_at(mt, f + 1);
                 }
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
@@ -409,10 +427,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
                     const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[mt], bfrag,
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag_buf[f & 1][mt], bfrag,
                                                                              acc[mt][j], 0, 0, 0);
                 }
             }
+            // Refill this ring slot only now that its codes are consumed: a load
+            // issued while the old value is live would land in other registers
+            // and be copied back (a wait on the load) at the loop edge.
+            __builtin_amdgcn_sched_barrier(0);
+            load_codes(kb + S, ring_codes[st], ring_meta[st]);
+            __builtin_amdgcn_sched_barrier(0);
             // every wave finished reading this LDS stage before it is rewritten
             // two blocks later (the next barrier orders it)
             __builtin_amdgcn_s_waitcnt(0xC07F);
