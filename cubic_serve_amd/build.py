@@ -69,6 +69,12 @@ def build(verbose: bool = False, jobs: int = 3) -> Path:
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if res.returncode != 0:
         raise RuntimeError("HIP link failed:\n" + res.stdout.decode(errors="replace"))
+    # every symbol must resolve now (a kernel whose host pass was dropped
+    # leaves an undefined launch stub that only shows at load time)
+    res = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], stdout=subprocess.PIPE)
+    stubs = [ln for ln in res.stdout.decode().splitlines() if "device_stub" in ln]
+    if stubs:
+        raise RuntimeError("HIP link left undefined kernel stubs:\n" + "\n".join(stubs[:10]))
     os.replace(tmp, LIB)
     return LIB
 
