@@ -52,14 +52,13 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
     p.k_blocks = (int)ceil_div(k, kKBlock);
     p.tiles_per_wave = 1;
     // Two 16-column tiles per wave once that still leaves >= 128 column
-    // blocks (halves the activation-fragment LDS reads per weight byte); four
-    // would drop to one wave per SIMD (register bound) and lose the VALU/MFMA
-    // overlap.
-    if (ceil_div(p.n_tiles, 8) >= 128) p.tiles_per_wave = 2;
+    // blocks (halves the activation bytes and A-fragment LDS reads per weight
+    // byte); four would drop to one wave per SIMD (register bound).
+    if (ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) >= 128) p.tiles_per_wave = 2;
 #ifdef CUBIC_TIMELINE  // instrumented build only: plan overrides for sweeps
     if (const char* e = getenv("CUBIC_DEV_J")) p.tiles_per_wave = atoi(e);
 #endif
-    p.col_blocks = (int)ceil_div(p.n_tiles, 4 * p.tiles_per_wave);
+    p.col_blocks = (int)ceil_div(p.n_tiles, cubic::kGemmWaves * p.tiles_per_wave);
     // K is split until about 256 workgroups are in flight (one per CU): more
     // partitions cost more in the exchange than they gain in parallelism.
     const int64_t out_blocks = (int64_t)p.col_blocks * ceil_div(m, 64);
@@ -76,13 +75,13 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
 }
 
 // Split-K partials: per K partition and output block (64-row chunk x column
-// block), 4 waves x J tiles x MT m-tiles x 64 lanes float4 units.
+// block), kGemmWaves waves x J tiles x MT m-tiles x 64 lanes float4 units.
 int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
     const GemmPlan p = plan_gemm(m, n, k);
     if (p.split == 1) return 0;
     const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, 64);
     const int64_t mt = ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1));
-    const int64_t units = 4 * p.tiles_per_wave * mt * 64;
+    const int64_t units = cubic::kGemmWaves * p.tiles_per_wave * mt * 64;
     return align256(blocks * 4) + align256((int64_t)p.split * blocks * units * 16);
 }
 

@@ -6,6 +6,12 @@
 
 namespace cubic {
 
+// GEMM workgroup: kGemmWaves waves, each owning J 16-column tiles, share one
+// LDS activation tile.  Four: two independent workgroups per CU hide latency
+// better than one 8-wave workgroup in barrier lockstep, although the latter
+// halves the activation bytes per weight byte (measured both).
+constexpr int kGemmWaves = 4;
+
 struct AcceptArgs {
     const uint16_t* logits;       // [rows, row_stride] bf16
     int64_t row_stride;           // elements

@@ -42,7 +42,8 @@ namespace cubic {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                  // prepare / expand kernels
+constexpr int kGemmThreads = kGemmWaves * 64;  // gemm_kernel
 constexpr int kKBlock = 128;
 // Activation stage in LDS: per 16-row block, 16-byte chunk c (k = 8c..8c+7 of
 // the k-block) of row r sits in 16-byte slot c * 16 + (r ^ c).  An MFMA
@@ -187,7 +188,7 @@ __device__ __forceinline__ uint4 direct_fragment(const uint32_t* w, int f, float
 
 // ---------------------------------------------------------------------------
 // GEMM kernel
-//   grid.x: column blocks of 4 waves x J tiles x 16 columns
+//   grid.x: column blocks of kGemmWaves waves x J tiles x 16 columns
 //   grid.y: K partitions (split)
 //   grid.z: 64-row chunks of M
 // ---------------------------------------------------------------------------
@@ -235,16 +236,16 @@ __device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buff
         for (int b = 0; b < kBatch; ++b)
 #pragma unroll
             for (int sp = 0; sp < S; ++sp)
-                v[b][sp] = load_device4(part, sp * split_bytes + ((b0 + b) * kThreads + threadIdx.x) * 16);
+                v[b][sp] = load_device4(part, sp * split_bytes + ((b0 + b) * kGemmThreads + threadIdx.x) * 16);
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
             floatx4_dev_t sum = v[b][0];
 #pragma unroll
             for (int sp = 1; sp < S; ++sp) sum += v[b][sp];
-            const int u = (b0 + b) * kThreads + threadIdx.x;
+            const int u = (b0 + b) * kGemmThreads + threadIdx.x;
             const int uw = u / (J * MT * kWave), uj = (u / (MT * kWave)) % J;
             const int umt = (u / kWave) % MT, ul = u % kWave;
-            const int n = ((blockIdx.x * 4 + uw) * J + uj) * 16 + (ul & 15);
+            const int n = ((blockIdx.x * kGemmWaves + uw) * J + uj) * 16 + (ul & 15);
             if (n >= a.n) continue;
             uint16_t* y = n < a.n_split ? a.y0 + n : a.y1 + (n - a.n_split);
             const int64_t ldy = n < a.n_split ? a.ldy0 : a.ldy1;
@@ -258,7 +259,7 @@ __device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buff
 }
 
 template <int BITS, int MT, int J, bool G128>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
     constexpr int S = Stages<BITS, J>::value;
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
@@ -266,14 +267,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int q = lane >> 4, col = lane & 15;
-    const int tile0 = (blockIdx.x * 4 + wave) * J;
+    const int tile0 = (blockIdx.x * kGemmWaves + wave) * J;
     const int split = blockIdx.y;
     const int m0 = blockIdx.z * 64;
     const int kb_begin = split * a.blocks_per_split;
     const int kb_end = min(kb_begin + a.blocks_per_split, a.k_blocks);
 
     if constexpr (BITS >= 5) {
-        for (int i = threadIdx.x; i < (1 << (BITS - 1)); i += kThreads)
+        for (int i = threadIdx.x; i < (1 << (BITS - 1)); i += kGemmThreads)
             t_lds[i] = (float)((double)i / (double)((1 << (BITS - 1)) - 1));
         __syncthreads();
     }
@@ -301,7 +302,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
     uint32_t ring_meta[S][J][MW];
     auto load_codes = [&](int kb, uint32_t (&codes)[J][W], uint32_t (&meta)[J][MW]) {
         kb = min(kb, kb_end - 1);
-        const int g = (kb * kKBlock + gq) / a.group_in;
+        // quarters past K (group_in < 128 with a K tail) would index one group
+        // past the last; their codes are zero padding against zero
+        // activations, so any in-bounds table serves
+        const int g = min((kb * kKBlock + gq) / a.group_in, a.groups_k - 1);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             load_words<W>(code_base[j] + kb * (kWave * W), codes[j]);
@@ -315,29 +319,30 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
             }
         }
     };
-    // activations: 64 rows x 128 k = 1024 chunks of 8 bf16, 4 per thread.
+    // activations: 16 * MT rows x 128 k, chunks of 8 bf16; thread t loads
+    // chunk t + kGemmThreads * i (row chunk / 16, k = 8 * (chunk % 16)), i < kAct.
     // k % 8 == 0 (admission): a chunk is wholly inside or outside K; rows past
     // M read row M-1 (their outputs are discarded), chunks past K are zero.
+    // With MT = 1 threads also load rows 16..31 (never read by the MFMAs).
     // Two register stages: the block for kb + 2 is in flight while kb is used.
-    uint4 act[2][4];
-    const uint16_t* act_row[4];
-    int act_c8[4];
+    constexpr int kAct = (16 * MT * 16 + kGemmThreads - 1) / kGemmThreads;
+    uint4 act[2][kAct];
+    const uint16_t* act_row[kAct];
+    int act_r[kAct];
+    const int act_c8 = (threadIdx.x & 15) * 8;  // same chunk column for every i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int chunk = threadIdx.x + kThreads * i;
-        const int r = chunk >> 4;
-        act_c8[i] = (chunk & 15) * 8;
-        act_row[i] = a.x + (int64_t)min(m0 + r, a.m - 1) * a.ldx + act_c8[i];
+    for (int i = 0; i < kAct; ++i) {
+        act_r[i] = (threadIdx.x + kGemmThreads * i) >> 4;
+        act_row[i] = a.x + (int64_t)min(m0 + act_r[i], a.m - 1) * a.ldx + act_c8;
     }
-    // rows 16*MT.. are not needed: chunk i covers rows 16i..16i+15, so only i < MT
     // The loaded registers are carried unmodified (any use right after the
     // load would make the wave wait for it); chunks past K read chunk 0 and
     // are zeroed when written to LDS.
-    auto load_act = [&](int kb, uint4 (&dst)[4]) {
+    auto load_act = [&](int kb, uint4 (&dst)[kAct]) {
         const int kofs = min(kb, kb_end - 1) * kKBlock;
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
-            dst[i] = *reinterpret_cast<const uint4*>(act_row[i] + (kofs + act_c8[i] < a.k ? kofs : 0));
+        for (int i = 0; i < kAct; ++i)
+            dst[i] = *reinterpret_cast<const uint4*>(act_row[i] + (kofs + act_c8 < a.k ? kofs : 0));
     };
 
     CUBIC_STAMP(0);
@@ -357,12 +362,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
             const int ab = st & kStageMask;  // S is even: the stage alternates every block
             uint16_t* lds = a_lds[ab];
             const uint32_t keep =  // same for all i
-                kb < kb_end && kb * kKBlock + act_c8[0] < a.k ? 0xFFFFFFFFu : 0u;
+                kb < kb_end && kb * kKBlock + act_c8 < a.k ? 0xFFFFFFFFu : 0u;
 #pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int r = (threadIdx.x >> 4) + 16 * i;
+            for (int i = 0; i < kAct; ++i) {
+                const int r = act_r[i];
                 const uint4 v = act[ab][i];
-                *reinterpret_cast<uint4*>(&lds[(i * 256 + a_slot(r & 15, act_c8[i] >> 3)) * 8]) =
+                *reinterpret_cast<uint4*>(&lds[((r >> 4) * 256 + a_slot(r & 15, act_c8 >> 3)) * 8]) =
                     make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
             }
             uint32_t codes[J][W];
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs a) {
     // split-K: each workgroup stores its FP32 accumulators in the MFMA-native
     // layout (one 16-byte unit per tile, m-tile and lane); the last arrival
     // sums the K partitions in ascending order.
-    constexpr int kUnits = 4 * J * MT * kWave;  // float4 units per output block
+    constexpr int kUnits = kGemmWaves * J * MT * kWave;  // float4 units per output block
     const int block = blockIdx.z * gridDim.x + blockIdx.x;
     const int split_bytes = (int)(gridDim.x * gridDim.z) * kUnits * 16;  // < 2^31: split > 1 only below 256 blocks of <= 64 KiB
     const __amdgpu_buffer_rsrc_t part =
@@ -664,10 +669,10 @@ __global__ void expand_metadata_kernel(int fmt, const void* m0, const void* m1, 
 template <int BITS, int MT, bool G128>
 hipError_t launch_g(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
 #ifdef CUBIC_TIMELINE
-    if (j == 4) { gemm_kernel<BITS, MT, 4, G128><<<grid, kThreads, 0, s>>>(a); return hipGetLastError(); }
+    if (j == 4) { gemm_kernel<BITS, MT, 4, G128><<<grid, kGemmThreads, 0, s>>>(a); return hipGetLastError(); }
 #endif
-    if (j == 2) gemm_kernel<BITS, MT, 2, G128><<<grid, kThreads, 0, s>>>(a);
-    else gemm_kernel<BITS, MT, 1, G128><<<grid, kThreads, 0, s>>>(a);
+    if (j == 2) gemm_kernel<BITS, MT, 2, G128><<<grid, kGemmThreads, 0, s>>>(a);
+    else gemm_kernel<BITS, MT, 1, G128><<<grid, kGemmThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -694,7 +699,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     const int rows_chunks = (a.m + 63) / 64;
     const int mt_eff = rows_chunks > 1 ? 4 : mt;
     const int j = a.tiles_per_wave;  // chosen by the host plan
-    const int cols_per_block = 4 * j * 16;
+    const int cols_per_block = kGemmWaves * j * 16;
     dim3 grid((a.n + cols_per_block - 1) / cols_per_block, a.split, rows_chunks);
     switch (a.bits) {
         case 1: return launch_bits<1>(a, mt_eff, j, grid, s);
