@@ -20,6 +20,19 @@
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
 
+#ifdef CUBIC_TIMELINE
+// Development instrumentation (never built into the shipped library).
+__device__ uint64_t g_acc_timeline[4096][16];
+extern "C" __attribute__((visibility("default"))) int cubic_dev_acc_timeline(uint64_t* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_acc_timeline), sizeof(g_acc_timeline));
+}
+#define ACC_STAMP(slot) \
+    do { if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 4096) \
+        g_acc_timeline[blockIdx.x + gridDim.x * blockIdx.y][(slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define ACC_STAMP(slot) do {} while (0)
+#endif
+
 namespace cubic {
 namespace {
 
@@ -40,6 +53,19 @@ constexpr int64_t kInt64Max = 0x7FFFFFFFFFFFFFFFLL;
 __device__ __forceinline__ uint32_t order_key16(uint32_t u) {
     const uint32_t m = u & 0x7FFFu;
     return (u & 0x8000u) ? 0x8000u - m : 0x8000u + m;
+}
+
+// Two bf16 -> two order keys (low / high half), with packed 16-bit integer
+// ops: 0x8000 + |u| for positive, 0x8000 - |u| for negative (-0 == +0).
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t order_key16x2(uint32_t w) {
+    const u16x2_t mag = __builtin_bit_cast(u16x2_t, w & 0x7FFF7FFFu);
+    const u16x2_t bias = {0x8000, 0x8000};
+    const uint32_t pos = __builtin_bit_cast(uint32_t, (u16x2_t)(bias + mag));
+    const uint32_t neg = __builtin_bit_cast(uint32_t, (u16x2_t)(bias - mag));
+    const uint32_t sgn = __builtin_bit_cast(uint32_t, (i16x2_t)(__builtin_bit_cast(i16x2_t, w) >> 15));
+    return (sgn & neg) | (~sgn & pos);
 }
 
 __device__ __forceinline__ uint32_t key16_to_bf16(uint32_t k) {
@@ -572,8 +598,9 @@ __global__ __launch_bounds__(kThreads) void merge_prefix_kernel(const int64_t* d
 // Candidate tiles + group finalisation (plain candidates or fused verify).
 // --------------------------------------------------------------------------
 struct TileScratch {
-    uint32_t survivors[kWaves][kWave];
-    uint32_t wave_top[kWaves * kTop];
+    uint32_t survivors[kWaves][kWave] __attribute__((aligned(16)));
+    uint32_t wave_top[kWaves * kTop] __attribute__((aligned(16)));
+    uint32_t tile_top[kTop];
     uint32_t flags[kWaves];
     uint32_t last;
     // finalisation: candidates of the group rows (count <= 64, rows <= 9)
@@ -595,78 +622,117 @@ __device__ __forceinline__ uint32_t elem_composite(const uint4 (&raw)[EMAX], int
     return (order_key16(u) << 16) | (0xFFFFu - (uint32_t)idx);
 }
 
+// Returns whether any element of the lane's share is non-finite.
 template <int EMAX>
-__device__ void tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
+__device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          TileScratch& ts, int lane, int wave, uint32_t* out_top) {
-    // 1. lane maxima
-    uint32_t lane_max = 0;
+    // 1. order keys, two per word (elements 2w, 2w + 1 of a chunk), 0 = empty;
+    //    a half is non-finite iff its magnitude is >= 0x7F80
+    uint32_t key2[EMAX][4];
+    uint32_t nonfinite = 0;
+    const bool partial = chunks * kChunk > width_left;  // wave-uniform
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-        if (e >= chunks) break;
+    for (int e = 0; e < EMAX; ++e)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
-            lane_max = c > lane_max ? c : lane_max;
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t word = (&raw[e].x)[w];
+            uint32_t valid = e < chunks ? 0xFFFFFFFFu : 0u;
+            if (partial) {
+                const int idx = (int)base_idx + e * kChunk + 2 * w;
+                valid &= (idx < width_left ? 0x0000FFFFu : 0u) | (idx + 1 < width_left ? 0xFFFF0000u : 0u);
+            }
+            const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
+            const u16x2_t inf = {0x7F80, 0x7F80};
+            nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
+            key2[e][w] = order_key16x2(word) & valid;
         }
-    }
-    // 2. threshold: the kTop-th largest lane maximum bounds the kTop-th element
-    const uint32_t sorted = wave_sort_desc(lane_max, lane);
-    const uint32_t tau = __shfl(sorted, kTop - 1);
-    // 3. survivors (>= tau; 0 is the empty key)
-    int mine = 0;
+    ACC_STAMP(11);
+    // 2. lane maxima (packed), then tau16 = the kTop-th largest lane maximum
+    //    (ballot radix select): kTop lanes hold distinct elements of value
+    //    >= tau16, so every element of the top kTop has a key >= tau16.
+    u16x2_t m2 = {0, 0};
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-        if (e >= chunks) break;
+    for (int e = 0; e < EMAX; ++e)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
-            mine += (c != 0u && c >= tau);
+        for (int w = 0; w < 4; ++w) {
+            const u16x2_t k = __builtin_bit_cast(u16x2_t, key2[e][w]);
+            m2 = k > m2 ? k : m2;
         }
+    const uint32_t lane_max = m2.x > m2.y ? m2.x : m2.y;
+    uint32_t tau = 0;
+#pragma unroll
+    for (int b = 15; b >= 0; --b) {
+        const uint32_t cand = tau | (1u << b);
+        if (__popcll(__ballot(lane_max >= cand)) >= kTop) tau = cand;
     }
-    // exclusive prefix over lanes
-    int incl = mine;
+    const uint32_t thr = tau > 0u ? tau : 1u;  // empty elements never survive
+    ACC_STAMP(12);
+    // 3. compact survivors (key >= thr) as composites, in element order; words
+    //    without a survivor in any lane are skipped with one wave-wide test
+    uint32_t total = 0;  // wave-uniform
+    const u16x2_t thr2 = {(unsigned short)thr, (unsigned short)thr};
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-    }
-    const int total = __shfl(incl, kWave - 1);
-    uint32_t top;
-    if (total <= kWave) {
-        int pos = incl - mine;
+    for (int e = 0; e < EMAX; ++e)
 #pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-            if (e >= chunks) break;
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t k2 = key2[e][w];
+            const uint32_t hit =
+                __builtin_bit_cast(uint32_t, (i16x2_t)(__builtin_bit_cast(u16x2_t, k2) >= thr2));
+            if (!__ballot(hit != 0u)) continue;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
-                if (c != 0u && c >= tau) ts.survivors[wave][pos++] = c;
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t k = h ? k2 >> 16 : k2 & 0xFFFFu;
+                const uint64_t m = __ballot(k >= thr);
+                if (m) {
+                    const uint32_t pos = total + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                    const uint32_t idx = base_idx + (uint32_t)(e * kChunk + 2 * w + h);
+                    if (k >= thr && pos < kWave) ts.survivors[wave][pos] = (k << 16) | (0xFFFFu - idx);
+                    total += (uint32_t)__popcll(m);
+                }
             }
         }
+    ACC_STAMP(13);
+    if (lane < kTop) out_top[lane] = 0u;
+    if (total <= kWave) {
+        // zero padding up to a multiple of 4 (slots past the survivors)
+        if (lane >= (int)total && lane < (int)((total + 3u) & ~3u)) ts.survivors[wave][lane] = 0u;
         wave_lds_sync();
-        const uint32_t v = lane < total ? ts.survivors[wave][lane] : 0u;
-        top = wave_sort_desc(v, lane);
+        // 4. rank by counting (composites are distinct): rank r -> slot r
+        const uint32_t v = lane < (int)total ? ts.survivors[wave][lane] : 0u;
+        uint32_t rank = 0;
+        for (uint32_t i = 0; i < total; i += 4) {
+            const uint4 w = *reinterpret_cast<const uint4*>(&ts.survivors[wave][i]);
+            rank += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
+        }
+        wave_lds_sync();
+        ACC_STAMP(14);
+        if (lane < (int)total && rank < (uint32_t)kTop) out_top[rank] = v;
     } else {
-        // many equal keys: kTop rounds of "largest composite below the previous"
+        // many equal values: kTop rounds of "largest composite below the previous"
         uint32_t prev = 0xFFFFFFFFu, mine_top = 0u;
         for (int round = 0; round < kTop; ++round) {
             uint32_t best = 0u;
 #pragma unroll
-            for (int e = 0; e < EMAX; ++e) {
-                if (e >= chunks) break;
+            for (int e = 0; e < EMAX; ++e)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t c = elem_composite<EMAX>(raw, e, j, base_idx, width_left);
+                    // recomputed every round: hoisting 64 composites out of the
+                    // round loop would cost 64 registers for a rare path
+                    uint32_t kw = key2[e][j >> 1];
+                    __asm__ volatile("" : "+v"(kw));
+                    const uint32_t k = j & 1 ? kw >> 16 : kw & 0xFFFFu;
+                    const uint32_t c = k ? (k << 16) | (0xFFFFu - (base_idx + (uint32_t)(e * kChunk + j))) : 0u;
                     if (c < prev && c > best) best = c;
                 }
-            }
             best = wave_max_u32(best);
             if (lane == round) mine_top = best;
             prev = best;
         }
-        top = mine_top;
+        wave_lds_sync();
+        if (lane < kTop) out_top[lane] = mine_top;
     }
-    if (lane < kTop) out_top[lane] = top;
+    return nonfinite != 0u;
 }
 
 template <int EMAX, bool FUSED, int SLOTS>
@@ -681,8 +747,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     const int chunks = (width_left + kChunk - 1) / kChunk;
     const uint16_t* src = a.logits + (int64_t)row * a.row_stride + begin;
 
+    ACC_STAMP(0);
     uint4 raw[EMAX];
-    uint32_t finite_acc = 0;
     if (owned) {
         const bool vec = a.vector_loads != 0;
 #pragma unroll
@@ -699,49 +765,46 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 raw[e] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-            if (e >= chunks) break;
-            const int off = e * kChunk + threadIdx.x * 8;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t word = (&raw[e].x)[j >> 1];
-                const uint32_t u = (j & 1) ? (word >> 16) : (word & 0xFFFFu);
-                finite_acc |= (off + j < width_left && nonfinite_bf16(u)) ? 1u : 0u;
-            }
-        }
     } else {
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) raw[e] = make_uint4(0, 0, 0, 0);
     }
+    ACC_STAMP(1);
     // wave top-kTop of this wave's share, then the workgroup's top-kTop
     const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
-    tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane, wave,
-                   &ts.wave_top[wave * kTop]);
-    const uint32_t bad = __any(finite_acc != 0);
+    const bool nonfinite = tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane,
+                                          wave, &ts.wave_top[wave * kTop]);
+    const uint32_t bad = __any(nonfinite);
     if (lane == 0) ts.flags[wave] = bad;
     __syncthreads();
+    ACC_STAMP(2);
     uint32_t* part = a.partial_keys + ((int64_t)row * a.tiles + tile) * kTop;
-    if (wave == 0) {
-        uint32_t v0 = lane < kTop * kWaves ? ts.wave_top[lane] : 0u;
-        uint32_t v1 = lane + kWave < kTop * kWaves ? ts.wave_top[lane + kWave] : 0u;
-        uint32_t prev = 0xFFFFFFFFu, my = 0u;
-        for (int round = 0; round < kTop; ++round) {
-            uint32_t b = 0u;
-            if (v0 < prev && v0 > b) b = v0;
-            if (v1 < prev && v1 > b) b = v1;
-            b = wave_max_u32(b);
-            if (lane == round) my = b;
-            prev = b;
+    // workgroup top-kTop: every wave ranks its kTop entries among all
+    // kWaves * kTop (nonzero composites are distinct; zeros are padding)
+    if (threadIdx.x < kTop) ts.tile_top[threadIdx.x] = 0u;
+    __syncthreads();
+    if (lane < kTop) {
+        const uint32_t v = ts.wave_top[wave * kTop + lane];
+        uint32_t rank = 0;
+#pragma unroll 4
+        for (int i = 0; i < kWaves * kTop; i += 4) {
+            const uint4 w = *reinterpret_cast<const uint4*>(&ts.wave_top[i]);
+            rank += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
         }
-        if (lane < kTop) store_device(&part[lane], my);
+        if (v != 0u && rank < (uint32_t)kTop) ts.tile_top[rank] = v;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (lane < kTop) store_device(&part[lane], ts.tile_top[lane]);
         if (lane == 0)
             store_device(&a.partial_flags[(int64_t)row * a.tiles + tile],
                          ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3]);
     }
     // arrival: the last workgroup of this row group finalises it
     const int group = row / a.group_rows;
-    if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) return;
+    ACC_STAMP(3);
+    if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) { ACC_STAMP(4); return; }
+    ACC_STAMP(5);
 
     // ---- finalise the group's rows: merge tiles, publish candidates -------
     const int row0 = group * a.group_rows;
@@ -767,8 +830,10 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 }
             }
         }
+        if (gr == 0) ACC_STAMP(6);
         const int want = a.count < kTop ? a.count : kTop;
         const uint64_t my = wave_topk_u64<kPer>(entry, a.tiles * kTop, want, lane, ts.merge[wave]);
+        if (gr == 0) ACC_STAMP(7);
         const float temp = a.row_temperatures[r];
         const bool greedy_pub = temp == 0.0f;
         const int j = lane;  // capacity <= 64
@@ -797,9 +862,11 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     }
     if (!FUSED) {
         if (threadIdx.x == 0) store_device(&a.counters[group], 0u);
+        ACC_STAMP(8);
         return;
     }
     __syncthreads();
+    ACC_STAMP(8);
     // ---- fused: verify each depth of sequence `group`, merge the prefix ----
     const int c = group, depth = a.group_rows - 1;
     for (int d = wave; d < depth; d += kWaves) {
@@ -833,6 +900,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
     }
     __syncthreads();
+    ACC_STAMP(9);
     if (threadIdx.x == 0) {
         int64_t accepted = depth, bonus = ts.decisions[depth - 1][1];
         bool good = true;
@@ -854,6 +922,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
         store_device(&a.counters[group], 0u);
     }
+    ACC_STAMP(10);
 }
 
 template <int EMAX, bool FUSED>

@@ -147,6 +147,9 @@ bool plan_tiles(int rows, int width, TilePlan* out) {
     int64_t tw = ceil_div(ceil_div(width, target), kChunk) * kChunk;
     const int64_t min_tw = ceil_div(ceil_div(width, kMaxTiles), kChunk) * kChunk;
     if (tw > (int64_t)kChunk * kMaxTileChunks) tw = (int64_t)kChunk * kMaxTileChunks;
+    // tiles of <= 8 chunks keep the per-lane element registers of the tile
+    // phase free of spills; wider tiles only when the tile count demands it
+    if (tw > (int64_t)kChunk * 8) tw = (int64_t)kChunk * 8;
     if (tw < min_tw) tw = min_tw;
     if (tw > (int64_t)kChunk * kMaxTileChunks) return false;
     out->tile_width = (int)tw;
