@@ -184,3 +184,28 @@ def test_lm_head_cfg2_shape_sampled_enclosure(oracle):
     for start in (0, 75968, n - 256):
         part = m.rows(start, start + 256).to("cpu")
         _check_linear(oracle, part, x, y[:, start:start + 256])
+
+
+def test_wide_output_repeatable_and_row_invariant(oracle):
+    """A wide output (640 column blocks: more than one round of resident
+    workgroups): enclosure on sampled column ranges, repeatability, and a
+    row's output independent of M up to 64 rows."""
+    n, k = 81920, 1024
+    g = torch.Generator(device=DEV).manual_seed(11)
+    m = qz.quantize_cubic(torch.randn((n, k), generator=g, device=DEV) * 0.02, bits=4, group_in=128)
+    x = torch.randn((64, k), generator=torch.Generator(device=DEV).manual_seed(12), device=DEV).to(torch.bfloat16)
+    out = torch.empty((64, n), dtype=torch.bfloat16, device=DEV)
+    ops = linear.PackedLinearOperators()
+    binding = ops.bind_linear(x, m, out)
+    binding.launch()
+    first = out.clone()
+    for _ in range(3):
+        out.zero_()
+        binding.launch()
+        assert torch.equal(out, first)
+    for start in (0, 512 * 128 - 128, 600 * 128, n - 256):
+        part = m.rows(start, start + 256).to("cpu")
+        _check_linear(oracle, part, x, first[:, start:start + 256])
+    for mrows in (1, 2, 17, 33):
+        y = ops.linear(x[:mrows].contiguous(), m)
+        assert torch.equal(y, first[:mrows]), mrows
