@@ -254,6 +254,87 @@ int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const 
                        ldy1, workspace, workspace_bytes, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Routed experts (MoE)
+// ---------------------------------------------------------------------------
+int cubic_moe_pad_routes(const int32_t* counts, const int32_t* starts, const int32_t* block_starts,
+                         const int32_t* total_blocks, const int32_t* row_map, int experts, int routes,
+                         int block_m, int32_t* padded, int32_t* block_expert, int32_t* padded_total,
+                         void* stream) {
+    if (!counts || !starts || !block_starts || !total_blocks || !row_map || !padded || !block_expert ||
+        !padded_total)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (experts <= 0 || routes < 0 || (block_m != 16 && block_m != 32 && block_m != 64))
+        return fail(CUBIC_EINVAL, "moe pad: experts=%d routes=%d block_m=%d", experts, routes, block_m);
+    return hip_status(cubic::launch_pad_routes(counts, starts, block_starts, total_blocks, row_map, experts,
+                                               routes, block_m, padded, block_expert, padded_total,
+                                               (hipStream_t)stream),
+                      "cubic_moe_pad_routes launch");
+}
+
+int64_t cubic_moe_max_blocks(int64_t routes, int experts, int block_m) {
+    if (routes < 0 || experts <= 0 || block_m <= 0) return -1;
+    const int64_t active = routes < experts ? routes : experts;  // experts holding a route
+    return ceil_div(routes + active * (block_m - 1), block_m);
+}
+
+int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                   int64_t expert_code_words, int64_t expert_meta_words, const int32_t* padded,
+                   const int32_t* block_expert, const int32_t* padded_total, int64_t max_blocks,
+                   int block_m, int routes, int top_k, int64_t n, int64_t k, int bits, int group_in,
+                   void* y, int64_t ldy, void* stream) {
+    if (!x || !codes || !meta || !padded || !block_expert || !padded_total || !y)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (block_m != 16 && block_m != 32 && block_m != 64)
+        return fail(CUBIC_ENOTSUP, "block_m=%d not in {16, 32, 64}", block_m);
+    if (routes <= 0 || top_k <= 0 || routes % top_k || max_blocks <= 0 || max_blocks * block_m > (1 << 30) ||
+        n <= 0 || k <= 0 || n > (1 << 30) || k > (1 << 30))
+        return fail(CUBIC_EINVAL, "moe gemm extents: routes=%d top_k=%d blocks=%lld n=%lld k=%lld", routes,
+                    top_k, (long long)max_blocks, (long long)n, (long long)k);
+    if (bits < 1 || bits > 8) return fail(CUBIC_ENOTSUP, "bits=%d outside 1..8", bits);
+    if (group_in <= 0 || group_in % 32) return fail(CUBIC_ENOTSUP, "group_in=%d must be a multiple of 32", group_in);
+    if (k % 8 || ldx % 8 || ldx < k || !aligned16(x))
+        return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
+    if (ldy < n) return fail(CUBIC_EINVAL, "output leading dimension too small");
+    int64_t cw = 0, mw = 0;
+    cubic_prepared_words(n, k, bits, group_in, &cw, &mw);
+    if (expert_code_words < cw || expert_meta_words < mw)
+        return fail(CUBIC_EINVAL, "expert strides smaller than one prepared matrix");
+    // one 64-row chunk plan: J and no K split (routed launches have
+    // max_blocks x column blocks workgroups)
+    const GemmPlan p = plan_gemm(64 * 256, n, k);
+    cubic::GemmArgs a = {};
+    a.x = (const uint16_t*)x;
+    a.codes = codes;
+    a.meta = meta;
+    a.y0 = (uint16_t*)y;
+    a.ldx = ldx;
+    a.ldy0 = ldy;
+    a.m = (int)(max_blocks * block_m);
+    a.n = (int)n;
+    a.k = (int)k;
+    a.n_split = (int)n;
+    a.bits = bits;
+    a.group_in = group_in;
+    a.k_blocks = p.k_blocks;
+    a.groups_k = (int)ceil_div(k, group_in);
+    a.split = 1;
+    a.blocks_per_split = p.k_blocks;
+    a.n_tiles = p.n_tiles;
+    a.tiles_per_wave = p.tiles_per_wave;
+    a.routed = 1;
+    a.block_m = block_m;
+    a.padded = padded;
+    a.block_expert = block_expert;
+    a.padded_total = padded_total;
+    a.routes = routes;
+    a.top_k = top_k;
+    a.expert_code_stride = expert_code_words;
+    a.expert_meta_stride = expert_meta_words;
+    return hip_status(cubic::launch_gemm(a, (hipStream_t)stream), "cubic_moe_gemm launch");
+}
+
+
 int64_t cubic_candidates_workspace_bytes(int rows, int width) {
     return accept_workspace(rows, rows, width);
 }

@@ -73,11 +73,17 @@ struct GemmArgs {
     int split, blocks_per_split;  // K partitions and k-blocks per partition
     int n_tiles;                  // ceil(n / 16)
     int tiles_per_wave;           // J: 16-column tiles per wave (1, 2, 4)
-    // routed experts (MoE): rows of x gathered through row_map, one expert per m-block
-    const int32_t* row_map;       // [padded routes] source token row, -1 = padding
-    const int32_t* block_expert;  // [m-blocks] expert of each 16-route block
+    // routed experts (MoE, routed != 0): workgroup chunk z covers the
+    // 16 * MT padded route slots [z * 16 * MT, ...) of one expert
+    // (block_expert[z]); a slot holds a route ordinal, or `routes` for
+    // padding; input row = route / top_k, output row = route.  Chunks at or
+    // past *padded_total / (16 * MT) exit at once.
+    int routed, block_m;          // block_m: 16, 32 or 64 route slots per block
+    const int32_t* padded;        // [max blocks * 16 * MT] route ordinals
+    const int32_t* block_expert;  // [max blocks] expert of each block
+    const int32_t* padded_total;  // device: total blocks * 16 * MT
+    int routes, top_k;
     int64_t expert_code_stride, expert_meta_stride;  // uint32 words per expert
-    int routed_blocks;
 };
 
 hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s);
@@ -88,6 +94,11 @@ hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t
                           const uint16_t* b, int64_t n, int64_t k, int bits, int group_in,
                           uint32_t* codes, uint32_t* meta, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Routed-block table from compact routes (quantization/common/marlin/repack.py:253-277)
+hipError_t launch_pad_routes(const int32_t* counts, const int32_t* starts, const int32_t* block_starts,
+                             const int32_t* total_blocks, const int32_t* row_map, int experts,
+                             int routes, int block_m, int32_t* padded, int32_t* block_expert,
+                             int32_t* padded_total, hipStream_t s);
 // fmt 0: m0 scale f32, m1 a f16, m2 b f16; fmt 1: m0 scale i8, m1 ab u8, g0..g2
 // globals f32; fmt 2: m0 metadata u16, m1 curve_a f16, m2 curve_b f16.
 hipError_t launch_expand_metadata(int fmt, const void* m0, const void* m1, const void* m2,

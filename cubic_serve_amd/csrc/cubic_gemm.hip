@@ -269,7 +269,22 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     const int q = lane >> 4, col = lane & 15;
     const int tile0 = (blockIdx.x * kGemmWaves + wave) * J;
     const int split = blockIdx.y;
-    const int m0 = blockIdx.z * 64;
+    const int m0 = blockIdx.z * (a.routed ? 16 * MT : 64);
+    // routed: this chunk's expert, or nothing to do past the routed blocks
+    int expert = 0;
+    if (a.routed) {
+        if (m0 >= *a.padded_total) return;  // uniform: before any barrier
+        expert = a.block_expert[blockIdx.z];
+    }
+    // source row of local row r (rows past M / padding slots read a valid row;
+    // their outputs are discarded)
+    auto src_row = [&](int r) -> int64_t {
+        if (a.routed) {
+            const int route = a.padded[m0 + r];
+            return route < a.routes ? route / a.top_k : 0;
+        }
+        return min(m0 + r, a.m - 1);
+    };
     const int kb_begin = split * a.blocks_per_split;
     const int kb_end = min(kb_begin + a.blocks_per_split, a.k_blocks);
 
@@ -293,8 +308,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int nt = min(tile0 + j, a.n_tiles - 1);
-        code_base[j] = a.codes + ((int64_t)nt * a.k_blocks * kWave + lane) * W;
-        meta_base[j] = a.meta + ((int64_t)nt * a.groups_k * 16 + col) * meta_words<BITS>();
+        code_base[j] = a.codes + expert * a.expert_code_stride + ((int64_t)nt * a.k_blocks * kWave + lane) * W;
+        meta_base[j] = a.meta + expert * a.expert_meta_stride +
+                       ((int64_t)nt * a.groups_k * 16 + col) * meta_words<BITS>();
     }
     const int gq = G128 ? 0 : 32 * q;  // G128: group_in is a multiple of 128
     uint32_t ring_codes[S][J][W];
@@ -333,7 +349,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < kAct; ++i) {
         act_r[i] = (threadIdx.x + kGemmThreads * i) >> 4;
-        act_row[i] = a.x + (int64_t)min(m0 + act_r[i], a.m - 1) * a.ldx + act_c8;
+        act_row[i] = a.x + src_row(act_r[i]) * a.ldx + act_c8;
     }
     // The loaded registers are carried unmodified (any use right after the
     // load would make the wave wait for it); chunks past K read chunk 0 and
@@ -461,8 +477,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + mt * 16 + 4 * q + r;
-                    if (m < a.m) y[(int64_t)m * ldy] = (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
+                    const int lr = mt * 16 + 4 * q + r;
+                    const int m = a.routed ? a.padded[m0 + lr] : m0 + lr;
+                    if (m < (a.routed ? a.routes : a.m))
+                        y[(int64_t)m * ldy] = (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
                 }
         }
         return;
@@ -695,9 +713,10 @@ hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t 
 // host plan: J from n, the K split from the number of output blocks (so a
 // row's result is the same for every m up to one 64-row chunk).
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-    const int mt = a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1);
-    const int rows_chunks = (a.m + 63) / 64;
-    const int mt_eff = rows_chunks > 1 ? 4 : mt;
+    // routed: one grid chunk per padded route block (a.m = block capacity)
+    const int mt = a.routed ? a.block_m / 16 : (a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1));
+    const int rows_chunks = a.routed ? a.m / a.block_m : (a.m + 63) / 64;
+    const int mt_eff = a.routed || rows_chunks == 1 ? mt : 4;
     const int j = a.tiles_per_wave;  // chosen by the host plan
     const int cols_per_block = kGemmWaves * j * 16;
     dim3 grid((a.n + cols_per_block - 1) / cols_per_block, a.split, rows_chunks);
@@ -712,6 +731,32 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         case 8: return launch_bits<8>(a, mt_eff, j, grid, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+// Routed-block table (repack.py:253-277 semantics): expert e's compact routes
+// row_map[starts[e] ..) fill padded slots (block_starts[e] + b) * block_m + i;
+// slots past counts[e] hold `routes` (padding); block_expert[block] = e.
+__global__ void pad_routes_kernel(const int32_t* counts, const int32_t* starts,
+                                  const int32_t* block_starts, const int32_t* total_blocks,
+                                  const int32_t* row_map, int routes, int block_m, int32_t* padded,
+                                  int32_t* block_expert, int32_t* padded_total) {
+    const int e = blockIdx.x;
+    const int count = counts[e], start = starts[e], block = block_starts[e];
+    const int blocks = (count + block_m - 1) / block_m;
+    for (int i = threadIdx.x; i < blocks * block_m; i += blockDim.x) {
+        padded[block * block_m + i] = i < count ? row_map[start + i] : routes;
+        if (i % block_m == 0) block_expert[block + i / block_m] = e;
+    }
+    if (e == 0 && threadIdx.x == 0) *padded_total = *total_blocks * block_m;
+}
+
+hipError_t launch_pad_routes(const int32_t* counts, const int32_t* starts, const int32_t* block_starts,
+                             const int32_t* total_blocks, const int32_t* row_map, int experts,
+                             int routes, int block_m, int32_t* padded, int32_t* block_expert,
+                             int32_t* padded_total, hipStream_t s) {
+    pad_routes_kernel<<<experts, kThreads, 0, s>>>(counts, starts, block_starts, total_blocks, row_map,
+                                                   routes, block_m, padded, block_expert, padded_total);
+    return hipGetLastError();
 }
 
 hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t* av,

@@ -92,6 +92,40 @@ CUBIC_API int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* cod
                        int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Routed experts (MoE).  Replaces the Cubic Marlin MoE bind
+ * (quantization/extensions/cubic/marlin.py:84-253: bind_grouped, bind_routed)
+ * with its route padding (quantization/common/marlin/repack.py:253-277,
+ * _pad_routes) over RoutedRows (quantization/api.py:123-134).
+ *
+ * cubic_moe_pad_routes: expert e's compact routes row_map[starts[e] ..
+ *   starts[e] + counts[e]) fill padded slots (block_starts[e] + b) * block_m
+ *   + i; slots past counts[e] hold `routes` (padding); block_expert[block] =
+ *   e; *padded_total = *total_blocks * block_m.  All int32, device.
+ *   block_starts are in units of block_m.
+ * cubic_moe_max_blocks: capacity of the padded tables, in blocks, for
+ *   `routes` routes over `experts` experts (routes + active experts x
+ *   (block_m - 1), rounded up).
+ * cubic_moe_gemm: y[route, :] = x[route / top_k, :] . decode(W[e])^T for every
+ *   route of every padded block of expert e (padding slots write nothing).
+ *   Expert e's prepared codes / metadata start at e * expert_code_words /
+ *   e * expert_meta_words.  Gate and up of one expert are prepared as one
+ *   [n_gate + n_up, k] matrix (columns gate first), as the reference groups
+ *   them.  block_m in {16, 32, 64}; top_k = 1 for the down projection.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_moe_pad_routes(const int32_t* counts, const int32_t* starts,
+                                   const int32_t* block_starts, const int32_t* total_blocks,
+                                   const int32_t* row_map, int experts, int routes, int block_m,
+                                   int32_t* padded, int32_t* block_expert, int32_t* padded_total,
+                                   void* stream);
+CUBIC_API int64_t cubic_moe_max_blocks(int64_t routes, int experts, int block_m);
+CUBIC_API int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                             int64_t expert_code_words, int64_t expert_meta_words,
+                             const int32_t* padded, const int32_t* block_expert,
+                             const int32_t* padded_total, int64_t max_blocks, int block_m,
+                             int routes, int top_k, int64_t n, int64_t k, int bits, int group_in,
+                             void* y, int64_t ldy, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Candidate preparation: vocab logits -> top-`count` candidates per row.
  * Replaces LocalCandidatePlan.launch (ops/cuda/sampling/local_candidates.py:
  * 206-226: torch.topk + candidate_partial/candidate_publish,
