@@ -51,6 +51,9 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the secondary configurations (cfg3 W3 lm_head + stochastic "
+                         "acceptance, cfg4 routed experts)")
     ap.add_argument("--cpu-rows", type=int, default=6144,
                     help="lm_head rows in the CPU-baseline sample")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
@@ -212,6 +215,91 @@ def cpu_baseline(step: dict, rows: int) -> dict:
                       f"[64,151936] logits ({t2 - t1:.2f}s); same algorithmic-byte accounting"}
 
 
+def measure_extras() -> dict:
+    """Secondary BASELINE configurations, one MI355X (not the headline value).
+
+    cfg3: W3 g128 lm_head 4096 -> 151936 at M = 256, and the fused stochastic
+    acceptance of batch 64 x k = 3 (T 0.7, top-p 0.9, top-k 20, seeded
+    uniforms) over N(0, 3) target logits, q candidates from target + N(0, 1).
+    cfg4: routed experts, 128 experts, top-8, hidden 2048, intermediate 768,
+    W4 g128, 256 tokens, router logits N(0, 1): gate/up and down launches.
+    Times are per launch (HIP events, graph replays); GB/s use the
+    algorithmic bytes of each launch.
+    """
+    import torch
+
+    from cubic_serve_amd import linear, moe, quantization as qz, sampling
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(20)
+    out = {}
+    # ---- cfg3 --------------------------------------------------------------
+    c, depth, rows = 64, 3, 64 * 4
+    w = torch.randn((VOCAB, HIDDEN), generator=g, device=dev) * 0.02
+    lm3 = linear.prepare_matrix(qz.quantize_cubic(w, bits=3, group_in=GROUP), dev)
+    del w
+    x = torch.randn((rows, HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((rows, VOCAB), dtype=torch.bfloat16, device=dev)
+    lm_b = linear.bind_prepared(x, lm3, (y,))
+    lm_ms = time_graph(capture(lm_b.launch), 20, 3)
+    target = (torch.randn((rows, VOCAB), generator=g, device=dev) * 3).to(torch.bfloat16)
+    draft_logits = (target.float().reshape(c, depth + 1, VOCAB)[:, :depth]
+                    + torch.randn((c, depth, VOCAB), generator=g, device=dev)).to(torch.bfloat16)
+    q_logits = draft_logits.permute(1, 0, 2).reshape(depth * c, VOCAB).contiguous()
+    del draft_logits
+    q_s = torch.empty((depth * c, 20), dtype=torch.bfloat16, device=dev)
+    q_i = torch.empty((depth * c, 20), dtype=torch.int64, device=dev)
+    sampling.LocalCandidatePlan(
+        local_logits=q_logits, workspace=sampling.ShardedSamplingWorkspace(q_s, q_i, q_s, q_i),
+        active_rows=depth * c, visible_width=VOCAB, local_count=20).launch(
+        temperatures=torch.full((depth * c,), 0.7, device=dev))
+    shape = (depth, c)
+    plan = sampling.MTPVerifyPlan(
+        logits=target, q_scores=q_s.reshape(depth, c, 20), q_token_ids=q_i.reshape(depth, c, 20),
+        draft_tokens=q_i[:, 0].reshape(shape).contiguous(),
+        temperatures=torch.full(shape, 0.7, device=dev), top_ps=torch.full(shape, 0.9, device=dev),
+        top_ks=torch.full(shape, 20, dtype=torch.int64, device=dev),
+        seeds=torch.randint(0, 2**40, shape, generator=g, device=dev),
+        ordinals=torch.randint(0, 10000, shape, generator=g, device=dev),
+        uniforms=torch.rand((depth, c, 2), generator=g, device=dev))
+    acc_ms = time_graph(capture(plan.launch), 50, 5)
+    accepted = plan.merged[:, 0].float()
+    out["cfg3"] = {"lm_head_w3_m256_us": round(lm_ms * 1e3, 2),
+                   "lm_head_w3_m256_gbs": round(gemm_bytes(rows, VOCAB, HIDDEN, 3) / lm_ms / 1e6, 1),
+                   "lm_head_w3_m256_tflops": round(2 * rows * VOCAB * HIDDEN / lm_ms / 1e9, 1),
+                   "accept_us": round(acc_ms * 1e3, 2),
+                   "accept_gbs": round(rows * VOCAB * 2 / acc_ms / 1e6, 1),
+                   "mean_accepted": round(float(accepted[accepted >= 0].mean()), 3)}
+    del target, q_logits, y, lm3
+    # ---- cfg4 --------------------------------------------------------------
+    experts, tokens, top_k, hidden, inter = 128, 256, 8, 2048, 768
+    quant = lambda n, k: qz.quantize_cubic(torch.randn((n, k), generator=g, device=dev) * 0.02,
+                                           bits=4, group_in=GROUP)
+    gate = tuple(quant(inter, hidden) for _ in range(experts))
+    up = tuple(quant(inter, hidden) for _ in range(experts))
+    down = tuple(quant(hidden, inter) for _ in range(experts))
+    xm = torch.randn((tokens, hidden), generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.argsort(torch.randn((tokens, experts), generator=g, device=dev), dim=-1,
+                        descending=True, stable=True)[:, :top_k]
+    routed = moe.route_rows(ids, experts, 32)
+    ops = linear.PackedLinearOperators()
+    h = torch.empty((tokens * top_k, 2 * inter), dtype=torch.bfloat16, device=dev)
+    _, b1 = moe.bind_grouped(ops, xm, gate, up, h, routed, top_k)
+    xd = torch.randn((tokens * top_k, inter), generator=g, device=dev).to(torch.bfloat16)
+    yd = torch.empty((tokens * top_k, hidden), dtype=torch.bfloat16, device=dev)
+    _, b2 = moe.bind_routed(ops, xd, down, yd, routed)
+    gu_ms = time_graph(capture(b1.launch), 20, 3)
+    dn_ms = time_graph(capture(b2.launch), 20, 3)
+    routes = tokens * top_k
+    gu_bytes = experts * (2 * inter * hidden // 2 + 2 * inter * (hidden // GROUP) * 8) + tokens * hidden * 2 + routes * 2 * inter * 2
+    dn_bytes = experts * (hidden * inter // 2 + hidden * (inter // GROUP) * 8) + routes * inter * 2 + routes * hidden * 2
+    out["cfg4"] = {"gate_up_us": round(gu_ms * 1e3, 2), "gate_up_gbs": round(gu_bytes / gu_ms / 1e6, 1),
+                   "down_us": round(dn_ms * 1e3, 2), "down_gbs": round(dn_bytes / dn_ms / 1e6, 1),
+                   "layer_us": round((gu_ms + dn_ms) * 1e3, 2),
+                   "layer_gbs": round((gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e6, 1)}
+    return out
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -310,6 +398,8 @@ def main(argv=None) -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_rows)
+    if not args.no_extras:
+        result["other_configs"] = measure_extras()
     print(json.dumps(result), flush=True)
     return 0
 
