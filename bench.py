@@ -223,6 +223,8 @@ def measure_extras() -> dict:
     uniforms) over N(0, 3) target logits, q candidates from target + N(0, 1).
     cfg4: routed experts, 128 experts, top-8, hidden 2048, intermediate 768,
     W4 g128, 256 tokens, router logits N(0, 1): gate/up and down launches.
+    embedding: packed lookup from a Qwen3-8B-shaped W4 g128 table (random
+    payload) for 64 tokens (one verify step) and 16384 tokens (prefill).
     Times are per launch (HIP events, graph replays); GB/s use the
     algorithmic bytes of each launch.
     """
@@ -297,6 +299,27 @@ def measure_extras() -> dict:
                    "down_us": round(dn_ms * 1e3, 2), "down_gbs": round(dn_bytes / dn_ms / 1e6, 1),
                    "layer_us": round((gu_ms + dn_ms) * 1e3, 2),
                    "layer_gbs": round((gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e6, 1)}
+    del gate, up, down, b1, b2, h, xd, yd
+    # ---- packed embedding (cfg2 model: Qwen3-8B table 151936 x 4096, W4 g128)
+    groups = (VOCAB, HIDDEN // GROUP)
+    table = qz.QuantizedMatrix(
+        {"weight_packed": torch.randint(0, 256, (VOCAB, HIDDEN // 2), generator=g, device=dev,
+                                        dtype=torch.int32).to(torch.uint8),
+         "weight_scale": torch.rand(groups, generator=g, device=dev) * 0.05,
+         "weight_a": (torch.rand(groups, generator=g, device=dev) * 1.5 - 0.25).half(),
+         "weight_b": (torch.rand(groups, generator=g, device=dev) - 0.5).half()},
+        qz.QuantizationScheme(qz.CUBIC_FORMAT, 4, GROUP), (VOCAB, HIDDEN))
+    row_bytes = HIDDEN // 2 + (HIDDEN // GROUP) * 8 + HIDDEN * 2 + 8  # codes, metadata, bf16 row, id
+    emb = {}
+    for tokens in (64, 16384):
+        tok = torch.randint(0, VOCAB, (tokens,), generator=g, device=dev)
+        rows_out = torch.empty((tokens, HIDDEN), dtype=torch.bfloat16, device=dev)
+        lookup = ops.bind_embedding(tok, table, rows_out)
+        # 20 lookups per graph: the per-lookup time, not the replay submission rate
+        ms = time_graph(capture(lambda: [lookup.launch() for _ in range(20)]), 10, 2) / 20
+        emb[f"m{tokens}_us"] = round(ms * 1e3, 2)
+        emb[f"m{tokens}_gbs"] = round(tokens * row_bytes / ms / 1e6, 1)
+    out["embedding"] = emb
     return out
 
 

@@ -254,6 +254,46 @@ int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const 
                        ldy1, workspace, workspace_bytes, stream);
 }
 
+int cubic_embedding(const void* ids, int id_bytes, int64_t tokens, int fmt, const void* packed,
+                    const void* m0, const void* m1, const void* m2, const void* g0, const void* g1,
+                    const void* g2, const int32_t* part_of_row, int64_t n, int64_t k, int bits,
+                    int group_in, int group_out, void* out, int out_dtype, void* stream) {
+    if (!ids || !packed || !m0 || !m1 || !out) return fail(CUBIC_EINVAL, "null operand");
+    if (id_bytes != 4 && id_bytes != 8) return fail(CUBIC_EINVAL, "embedding ids must be int32 or int64");
+    if (out_dtype != CUBIC_DTYPE_BF16 && out_dtype != CUBIC_DTYPE_F16)
+        return fail(CUBIC_EINVAL, "embedding output must be bf16 or fp16");
+    if (fmt < 0 || fmt > 2) return fail(CUBIC_ENOTSUP, "unknown metadata format %d", fmt);
+    if (tokens <= 0 || tokens > 0x7fffffff) return fail(CUBIC_EINVAL, "embedding needs 1 <= tokens < 2^31");
+    if (n <= 0 || k <= 0 || bits < 1 || bits > 8 || group_in <= 0) return fail(CUBIC_EINVAL, "invalid geometry");
+    if (group_out <= 0 || n % group_out) return fail(CUBIC_EINVAL, "group_out must divide n");
+    if (cubic::embedding_column_blocks(k) > 65535) return fail(CUBIC_ENOTSUP, "embedding width %lld too large", (long long)k);
+    if (fmt != 0 && !part_of_row) return fail(CUBIC_EINVAL, "format %d needs part_of_row", fmt);
+    if (fmt == 1 && (!g0 || !g1 || !g2)) return fail(CUBIC_EINVAL, "format 1 needs the partition globals");
+    if (fmt != 1 && !m2) return fail(CUBIC_EINVAL, "format %d needs its third metadata tensor", fmt);
+    cubic::EmbedArgs a = {};
+    a.ids = ids;
+    a.id_bytes = id_bytes;
+    a.tokens = tokens;
+    a.fmt = fmt;
+    a.packed = (const uint8_t*)packed;
+    a.m0 = m0; a.m1 = m1; a.m2 = m2;
+    a.g0 = g0; a.g1 = g1; a.g2 = g2;
+    a.part_of_row = part_of_row;
+    a.n = n;
+    a.k = k;
+    a.row_bytes = ceil_div(k * bits, 8);
+    a.groups_k = ceil_div(k, group_in);
+    a.bits = bits;
+    a.group_in = group_in;
+    a.group_out = group_out;
+    a.aligned = ((uintptr_t)packed % 4 == 0) && (a.row_bytes % 4 == 0);
+    a.chunk_in_group = group_in % 16 == 0;
+    a.lut = a.chunk_in_group && 4 * (1 << bits) <= group_in;
+    a.out = (uint16_t*)out;
+    a.out_fp16 = out_dtype == CUBIC_DTYPE_F16;
+    return hip_status(cubic::launch_embedding(a, (hipStream_t)stream), "cubic_embedding launch");
+}
+
 // ---------------------------------------------------------------------------
 // Routed experts (MoE)
 // ---------------------------------------------------------------------------

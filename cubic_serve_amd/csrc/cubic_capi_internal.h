@@ -86,6 +86,23 @@ struct GemmArgs {
     int64_t expert_code_stride, expert_meta_stride;  // uint32 words per expert
 };
 
+struct EmbedArgs {
+    const void* ids;              // [tokens] int32 or int64 (id_bytes)
+    int id_bytes;
+    int64_t tokens;
+    int fmt;                      // metadata format (group_metadata)
+    const uint8_t* packed;        // [n, row_bytes] little-endian bitstream
+    const void *m0, *m1, *m2, *g0, *g1, *g2;
+    const int32_t* part_of_row;   // [n] output partition of each row (fmt 1, 2)
+    int64_t n, k, row_bytes, groups_k;
+    int bits, group_in, group_out;
+    int aligned;                  // packed base and row_bytes 4-byte aligned
+    int chunk_in_group;           // group_in % 16 == 0: a 16-column chunk is in one group
+    int lut;                      // chunk_in_group and 4 * 2^bits <= group_in: table path
+    uint16_t* out;                // [tokens, k] bf16 or fp16
+    int out_fp16;
+};
+
 hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
 hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
@@ -106,5 +123,9 @@ hipError_t launch_expand_metadata(int fmt, const void* m0, const void* m1, const
                                   const int32_t* part_of_row,
                                   int64_t n, int64_t groups_k, int group_out, float* scale,
                                   uint16_t* a, uint16_t* b, hipStream_t s);
+
+// Packed embedding lookup (quantization/extensions/cubic/linear.py:266-294)
+hipError_t launch_embedding(const EmbedArgs& a, hipStream_t s);
+int64_t embedding_column_blocks(int64_t k);  // grid.y of launch_embedding
 
 }  // namespace cubic

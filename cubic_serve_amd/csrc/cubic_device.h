@@ -33,6 +33,53 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
 
+// fl32(m / D) with the division done in binary64 and rounded once to binary32,
+// as reference.py:120 does.  Evaluated at compile time for unrolled m.
+template <int BITS>
+__host__ __device__ constexpr float t_of(int m) {
+    return (float)((double)m / (double)((1 << (BITS - 1)) - 1));
+}
+
+// One Cubic level: s * (t * (a + t * (b + t * ((1 - a) - b)))), unfused fp32.
+__device__ __forceinline__ float curve_level(float t, float s, float a, float b) {
+    const float c = (1.0f - a) - b;
+    const float inner = b + t * c;
+    const float mid = a + t * inner;
+    return s * (t * mid);
+}
+
+// Per-group metadata of a Cubic payload as (scale f32, a f16 bits, b f16 bits)
+// (quantization/extensions/cubic/reference.py:67-95; the same roundings as
+// kernels.py:82-97).  src = (row / group_out) * groups_k + group; p = the
+// row's output partition.
+//   fmt 0: m0 scale f32, m1 a f16, m2 b f16
+//   fmt 1: m0 scale i8, m1 ab u8 (two signed nibbles), g0..g2 partition globals f32
+//   fmt 2: m0 e5m9 scale | curve << 14 u16, m1/m2 curve a/b f16 [partitions][4]
+__device__ __forceinline__ void group_metadata(int fmt, const void* m0, const void* m1, const void* m2,
+                                               const void* g0, const void* g1, const void* g2,
+                                               int64_t src, int p, float& scale, uint16_t& a,
+                                               uint16_t& b) {
+    if (fmt == 0) {
+        scale = ((const float*)m0)[src];
+        a = ((const uint16_t*)m1)[src];
+        b = ((const uint16_t*)m2)[src];
+    } else if (fmt == 1) {
+        const int8_t si = ((const int8_t*)m0)[src];
+        const uint32_t ab = ((const uint8_t*)m1)[src];
+        const int lo = (int)(ab & 15u), hi = (int)(ab >> 4);
+        const float af = (float)(lo >= 8 ? lo - 16 : lo), bf = (float)(hi >= 8 ? hi - 16 : hi);
+        scale = (float)si * ((const float*)g0)[p];
+        const float prod = af * ((const float*)g1)[p];
+        a = __half_as_ushort(__float2half_rn(1.0f + prod));
+        b = __half_as_ushort(__float2half_rn(bf * ((const float*)g2)[p]));
+    } else {
+        const uint32_t md = ((const uint16_t*)m0)[src];
+        scale = half_bits_to_float((md & 0x3FFFu) << 1);
+        a = ((const uint16_t*)m1)[p * 4 + (md >> 14)];
+        b = ((const uint16_t*)m2)[p * 4 + (md >> 14)];
+    }
+}
+
 // exp for the acceptance transform: Cody & Waite (1980) two-constant additive
 // reduction x = n*ln2 + r, |r| <= ln2/2, exp(r) by the degree-7 Taylor
 // polynomial in Horner form, times 2^n.  Unfused binary32 operations in a

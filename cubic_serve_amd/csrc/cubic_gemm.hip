@@ -61,21 +61,6 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// fl32(m / D) with the division done in binary64 and rounded once to binary32,
-// as reference.py:120 does.  Evaluated at compile time for unrolled m.
-template <int BITS>
-__host__ __device__ constexpr float t_of(int m) {
-    return (float)((double)m / (double)((1 << (BITS - 1)) - 1));
-}
-
-// One Cubic level: s * (t * (a + t * (b + t * ((1 - a) - b)))), unfused fp32.
-__device__ __forceinline__ float curve_level(float t, float s, float a, float b) {
-    const float c = (1.0f - a) - b;
-    const float inner = b + t * c;
-    const float mid = a + t * inner;
-    return s * (t * mid);
-}
-
 // Prepared metadata words per (column, group): bits <= 4 store the group's bf16
 // level table as v_perm byte planes (4 words at 4 bits, 2 words below);
 // bits >= 5 store (scale f32, a f16 | b f16 << 16).
@@ -662,25 +647,7 @@ __global__ void expand_metadata_kernel(int fmt, const void* m0, const void* m1, 
         const int64_t row = i / groups_k, g = i % groups_k;
         const int64_t src = (row / group_out) * groups_k + g;
         const int p = part_of_row ? part_of_row[row] : 0;
-        if (fmt == 0) {
-            scale[i] = ((const float*)m0)[src];
-            av[i] = ((const uint16_t*)m1)[src];
-            bv[i] = ((const uint16_t*)m2)[src];
-        } else if (fmt == 1) {
-            const int8_t si = ((const int8_t*)m0)[src];
-            const uint32_t ab = ((const uint8_t*)m1)[src];
-            const int lo = (int)(ab & 15u), hi = (int)(ab >> 4);
-            const float af = (float)(lo >= 8 ? lo - 16 : lo), bf = (float)(hi >= 8 ? hi - 16 : hi);
-            scale[i] = (float)si * ((const float*)g0)[p];
-            const float prod = af * ((const float*)g1)[p];
-            av[i] = __half_as_ushort(__float2half_rn(1.0f + prod));
-            bv[i] = __half_as_ushort(__float2half_rn(bf * ((const float*)g2)[p]));
-        } else {
-            const uint32_t md = ((const uint16_t*)m0)[src];
-            scale[i] = half_bits_to_float((md & 0x3FFFu) << 1);
-            av[i] = ((const uint16_t*)m1)[p * 4 + (md >> 14)];
-            bv[i] = ((const uint16_t*)m2)[p * 4 + (md >> 14)];
-        }
+        group_metadata(fmt, m0, m1, m2, g0, g1, g2, src, p, scale[i], av[i], bv[i]);
     }
 }
 

@@ -11,6 +11,7 @@ Host mirror of the reference's operator API (paths under src/cubic_serve/):
     bind_native                :123-131
     bind_linear                :134-263
     bind_grouped               :297-305
+    bind_embedding             :266-294   (operator side quantized.py:776-846)
 
 Every launch goes through the HIP library (include/cubic_mi355x.h); there is
 no eager fallback.  Weights are prepared once per matrix (codes repacked into
@@ -229,6 +230,51 @@ def bind_grouped(operators, x, weights, outputs, params=None):
     return operators._bind_gemm(x, tuple(weights), tuple(outputs))
 
 
+class _EmbeddingLaunch:
+    """One bound cubic_embedding call over a payload as stored."""
+
+    def __init__(self, input_ids: Tensor, weight: QuantizedMatrix, output: Tensor, parts: Tensor):
+        self.input_ids, self.weight, self.output, self.parts = input_ids, weight, output, parts
+        self.identity = self._identity()
+
+    def _identity(self):
+        return tuple((t.data_ptr(), tuple(t.shape), t.dtype) for t in
+                     (self.input_ids, self.output, *self.weight.payload.values()))
+
+    def validate(self) -> None:
+        if self._identity() != self.identity:
+            raise ValueError("packed launch operands changed after binding")
+
+    def __call__(self, stream: int) -> None:
+        w, e = self.weight, self.weight.encoding
+        p = w.payload
+        fmt = METADATA_IDS[e.metadata]
+        if fmt == 0:
+            meta = (p["weight_scale"], p["weight_a"], p["weight_b"], None, None, None)
+        elif fmt == 1:
+            meta = (p["weight_scale"], p["weight_ab"], None, p["weight_scale_global"],
+                    p["weight_a_global"], p["weight_b_global"])
+        else:
+            meta = (p["weight_metadata"], p["weight_curve_a"], p["weight_curve_b"], None, None, None)
+        n, k = w.shape
+        _native.call("cubic_embedding", self.input_ids.data_ptr(), self.input_ids.element_size(),
+                     self.input_ids.numel(), fmt, p["weight_packed"].data_ptr(),
+                     *(_native.ptr(t) for t in meta), self.parts.data_ptr(), n, k, e.bits,
+                     e.group_in, e.group_out, self.output.data_ptr(),
+                     1 if self.output.dtype == torch.float16 else 0, stream)
+
+
+def bind_embedding(operators, input_ids, weight, output, params=None):
+    """Cubic embedding hook (:266-294): decode the looked-up rows from the payload."""
+    if isinstance(params, CubicLinearParameters) and not params.native_enabled:
+        raise ValueError("Cubic native embedding is disabled and has no fallback")
+    key = ("cubic.mi355x.parts.v1", id(weight), str(input_ids.device))
+    cached = operators.prepared_weights.get(key)
+    if cached is None:
+        cached = operators.prepared_weights[key] = (weight, partition_rows(weight).to(input_ids.device))
+    return PackedOperatorBinding(output, (_EmbeddingLaunch(input_ids, weight, output, cached[1]),))
+
+
 class PackedLinearOperators:
     """Binds Cubic linears to native launches before capture (quantized.py:248)."""
 
@@ -310,6 +356,32 @@ class PackedLinearOperators:
         launches = tuple(l for w, y in zip(weights, outputs)
                          for l in bind_linear(self, x, w, y, params)._launches)
         return PackedOperatorBinding(outputs, launches)
+
+    def embedding(self, input_ids: Tensor, weight: QuantizedMatrix, *, dtype: torch.dtype) -> Tensor:
+        """Eager lookup (quantized.py:776-784)."""
+        output = torch.empty((*input_ids.shape, weight.shape[1]), dtype=dtype, device=input_ids.device)
+        self.bind_embedding(input_ids.contiguous(), weight, output).launch()
+        return output
+
+    def bind_embedding(self, input_ids: Tensor, weight: QuantizedMatrix, output: Tensor,
+                       params: CubicLinearParameters | None = None) -> PackedOperatorBinding:
+        """Bind a lookup; ids are read at launch (validation quantized.py:793-826)."""
+        if not isinstance(weight, QuantizedMatrix) or len(weight.shape) != 2:
+            raise ValueError("native Cubic embedding requires a packed matrix weight")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("Cubic embeddings must be bound before graph capture")
+        tensors = (input_ids, output, *weight.payload.values())
+        k = weight.shape[1]
+        if (not input_ids.is_cuda
+                or input_ids.dtype not in (torch.int32, torch.int64)
+                or input_ids.numel() <= 0
+                or output.dtype not in (torch.float16, torch.bfloat16)
+                or output.shape != (*input_ids.shape, k)
+                or any(t.device != input_ids.device or not t.is_contiguous() for t in tensors)):
+            raise ValueError("bound embedding requires contiguous same-device IDs, weight and FP16/BF16 output")
+        if any(_storage(output) == _storage(t) for t in (input_ids, *weight.payload.values())):
+            raise ValueError("bound embedding output must not alias its operands")
+        return bind_embedding(self, input_ids, weight, output, params)
 
     def linear(self, x: Tensor, weight: QuantizedMatrix) -> Tensor:
         """Eager convenience: bind, launch once, return the output."""

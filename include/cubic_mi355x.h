@@ -126,6 +126,29 @@ CUBIC_API int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, 
                              void* y, int64_t ldy, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Packed embedding lookup: out[t, :] = decode(W[ids[t], :]) rounded to the
+ * output dtype.  Replaces PackedLinearOperators.bind_embedding for Cubic
+ * matrices (ops/cuda/linear/quantized.py:786-846) and the Cubic hook
+ * bind_embedding (quantization/extensions/cubic/linear.py:266-294, kernel
+ * quantization/common/kernels.py:138-164 with load_weight,
+ * quantization/extensions/cubic/kernels.py:44-113).  Reads the checkpoint
+ * payload as stored (no preparation):
+ *   ids          int32 (id_bytes 4) or int64 (id_bytes 8) [tokens]; an id
+ *                outside [0, n) yields a zero row
+ *   fmt, packed, m0..m2, g0..g2, part_of_row: as cubic_prepare_weight
+ *   out          [tokens, k] contiguous, out_dtype CUBIC_DTYPE_BF16 / _F16
+ * Bit-exact to the reference decode: every value is evaluated in unfused
+ * binary32 in the reference's order and rounded once (RNE).
+ * ------------------------------------------------------------------------- */
+#define CUBIC_DTYPE_BF16 0
+#define CUBIC_DTYPE_F16 1
+CUBIC_API int cubic_embedding(const void* ids, int id_bytes, int64_t tokens, int fmt,
+                              const void* packed, const void* m0, const void* m1, const void* m2,
+                              const void* g0, const void* g1, const void* g2,
+                              const int32_t* part_of_row, int64_t n, int64_t k, int bits,
+                              int group_in, int group_out, void* out, int out_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Candidate preparation: vocab logits -> top-`count` candidates per row.
  * Replaces LocalCandidatePlan.launch (ops/cuda/sampling/local_candidates.py:
  * 206-226: torch.topk + candidate_partial/candidate_publish,

@@ -48,3 +48,15 @@ def test_invalid_arguments_fail_before_any_launch():
         _native.call("cubic_verify_candidates", *([16] * 13), 0, 9, 4, 8, 20, 4, 16, None)
     with pytest.raises(ValueError, match="group_in"):
         _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 100, 16, 4096, None, 0, None)
+    with pytest.raises(ValueError, match="int32 or int64"):
+        _native.call("cubic_embedding", 16, 2, 4, 0, 16, 16, 16, 16, None, None, None, None,
+                     64, 128, 4, 32, 1, 16, 0, None)
+    with pytest.raises(ValueError, match="bf16 or fp16"):
+        _native.call("cubic_embedding", 16, 8, 4, 0, 16, 16, 16, 16, None, None, None, None,
+                     64, 128, 4, 32, 1, 16, 2, None)
+    with pytest.raises(ValueError, match="part_of_row"):
+        _native.call("cubic_embedding", 16, 8, 4, 2, 16, 16, 16, 16, None, None, None, None,
+                     64, 128, 4, 32, 1, 16, 0, None)
+    with pytest.raises(ValueError, match="group_out"):
+        _native.call("cubic_embedding", 16, 8, 4, 0, 16, 16, 16, 16, None, None, None, None,
+                     64, 128, 4, 32, 3, 16, 0, None)
