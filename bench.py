@@ -225,6 +225,8 @@ def measure_extras() -> dict:
     W4 g128, 256 tokens, router logits N(0, 1): gate/up and down launches.
     embedding: packed lookup from a Qwen3-8B-shaped W4 g128 table (random
     payload) for 64 tokens (one verify step) and 16384 tokens (prefill).
+    root_sampler: top-k/top-p sampling of TP=4 x K=20 candidates for 1 and
+    256 rows (T 0.8, top-p 0.9, top-k 20).
     Times are per launch (HIP events, graph replays); GB/s use the
     algorithmic bytes of each launch.
     """
@@ -320,6 +322,21 @@ def measure_extras() -> dict:
         emb[f"m{tokens}_us"] = round(ms * 1e3, 2)
         emb[f"m{tokens}_gbs"] = round(tokens * row_bytes / ms / 1e6, 1)
     out["embedding"] = emb
+    # ---- root top-k/top-p sampler (topk_topp.py; the reference benchmarks C=1, C=256, TP=4 x K=20)
+    root = {}
+    for rows in (1, 256):
+        sc = torch.randn((4, rows, 20), generator=g, device=dev).to(torch.bfloat16)
+        ids = torch.arange(80, device=dev).view(4, 1, 20).expand(4, rows, 20).contiguous()
+        ops_r = (sc, ids, torch.full((rows,), 0.8, device=dev), torch.full((rows,), 0.9, device=dev),
+                 torch.full((rows,), 20, dtype=torch.int64, device=dev),
+                 torch.arange(rows, dtype=torch.int64, device=dev) + 0x123456789,
+                 torch.zeros(rows, dtype=torch.int64, device=dev),
+                 torch.empty(rows, dtype=torch.int64, device=dev),
+                 torch.empty(rows, dtype=torch.bool, device=dev))
+        prim = sampling.RootTopKTopPSamplingPrimitive(*ops_r)
+        ms = time_graph(capture(lambda: [prim.launch(*ops_r) for _ in range(20)]), 10, 2) / 20
+        root[f"c{rows}_us"] = round(ms * 1e3, 2)
+    out["root_sampler"] = root
     return out
 
 

@@ -38,6 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_candidates": (I32, [P, I64, I32, I32, P, I32, I32, I32, I32, P, P, P, I64, P]),
     "cubic_verify_candidates": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32,
                                       I32, I32, P, P]),
+    "cubic_root_sample": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P, P]),
     "cubic_merge_prefix": (I32, [P, I32, I32, P, I32, P, P]),
     "cubic_accept_workspace_bytes": (I64, [I32, I32, I32]),
     "cubic_accept": (I32, [P, I64, I32, I32, I32, I32, P, P, P, I32, P, P, P, P, P, P, P, P, P, P,

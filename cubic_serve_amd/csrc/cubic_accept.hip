@@ -378,7 +378,9 @@ __device__ int select_set(const LaneSet<SLOTS>& in, int block, int k, int lane,
 }
 
 // speculative.py:32-43 for one selected set (scores in rank order).
-template <int SLOTS>
+// NORMALIZE = false returns the retained probabilities before the division by
+// their mass (topk_topp.py:94-100 samples from those).
+template <int SLOTS, bool NORMALIZE = true>
 __device__ __forceinline__ void probabilities(const float (&sorted)[SLOTS], float temperature,
                                               int64_t top_k, float top_p, int block, int lane,
                                               float (&out)[SLOTS], float& mass) {
@@ -411,7 +413,7 @@ __device__ __forceinline__ void probabilities(const float (&sorted)[SLOTS], floa
     }
     mass = vl_tree_sum<SLOTS>(tmp, block);
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) out[s] = p[s] / mass;
+    for (int s = 0; s < SLOTS; ++s) out[s] = NORMALIZE ? p[s] / mass : p[s];
 }
 
 template <int SLOTS>
@@ -536,6 +538,110 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         out2[1] = valid ? next : -1;
     }
     wave_lds_sync();
+}
+
+// --------------------------------------------------------------------------
+// Root top-k/top-p sampling (ops/cuda/sampling/topk_topp.py:22-121).  One
+// workgroup per row, one thread per gathered candidate (TP * K <= 160):
+//   1. load; a pair is real (finite score, id >= 0) or the NaN/-1 sentinel;
+//   2. a real pair is first unless an earlier lane holds the same (score, id);
+//   3. the rank of a first pair = first pairs strictly ahead in (score desc,
+//      id asc); ranks < K land in LDS.  This is the reference's K rounds of
+//      max / min-id / remove-all-copies, as one counting pass;
+//   4. wave 0 runs temperature, softmax, top-p over the exclusive CDF and the
+//      inverse-CDF draw over the K ranked slots (slots past the selection are
+//      (-inf, INT64_MAX) and carry zero weight, so reducing over 64 lanes
+//      gives the same bits as over next_pow2(TP * K)).
+// Reduction orders and exp as verify_wave.
+// --------------------------------------------------------------------------
+constexpr int kRootThreads = 256;
+
+struct RootEntry {
+    float score;
+    uint32_t flags;  // bit 0 real, bit 1 first
+    int64_t id;
+};
+
+struct RootScratch {
+    RootEntry e[kRootThreads];
+    float sel_score[kWave];
+    int64_t sel_id[kWave];
+};
+
+__global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArgs a) {
+    __shared__ RootScratch sc;
+    const int row = blockIdx.x, v = threadIdx.x;
+    const int count = a.tp * a.k;
+    const bool cm = v < count;
+    float score = -__builtin_huge_valf();
+    int64_t id = -1;
+    if (cm) {
+        const int64_t off = ((int64_t)(v / a.k) * a.rows + row) * a.k + v % a.k;
+        const uint32_t bits = a.scores[off];
+        score = a.scores_fp16 ? half_bits_to_float(bits) : bf16_bits_to_float(bits);
+        id = a.ids[off];
+    }
+    const bool real = cm && id >= 0 && __builtin_fabsf(score) < __builtin_huge_valf();
+    const bool sentinel = cm && score != score && id == -1;
+    sc.e[v].score = score;
+    sc.e[v].id = id;
+    sc.e[v].flags = real ? 1u : 0u;
+    if (v < kWave) { sc.sel_score[v] = -__builtin_huge_valf(); sc.sel_id[v] = kInt64Max; }
+    const int malformed = __syncthreads_count(cm && !real && !sentinel);
+    const int real_count = __syncthreads_count(real);
+    // Branch-free passes over uniform (broadcast) LDS entries, unrolled so
+    // the reads of several entries are in flight together.
+    uint32_t dup = 0;
+#pragma unroll 8
+    for (int j = 0; j < count; ++j) {
+        const RootEntry o = sc.e[j];
+        dup |= (uint32_t)(j < v) & o.flags & (uint32_t)(o.score == score) & (uint32_t)(o.id == id);
+    }
+    const bool first = real && !dup;
+    __syncthreads();
+    if (first) sc.e[v].flags = 3u;
+    __syncthreads();
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < count; ++j) {
+        const RootEntry o = sc.e[j];
+        const uint32_t ahead = (uint32_t)(o.score > score) | ((uint32_t)(o.score == score) & (uint32_t)(o.id < id));
+        rank += (int)((o.flags >> 1) & ahead);
+    }
+    if (first && rank < a.k) { sc.sel_score[rank] = score; sc.sel_id[rank] = id; }
+    __syncthreads();
+    if (v >= kWave) return;
+
+    const int lane = v;
+    const float temperature = a.temperatures[row], top_p = a.top_ps[row];
+    const int64_t top_k = a.top_ks[row], seed = a.seeds[row], ordinal = a.ordinals[row];
+    const bool greedy = temperature == 0.0f;
+    const bool params_ok = temperature == temperature && temperature >= 0.0f &&
+                           temperature < __builtin_huge_valf() && top_p == top_p && top_p > 0.0f &&
+                           top_p <= 1.0f && top_k >= 1 && top_k <= a.k && seed >= 0 && ordinal >= 0;
+    bool under = a.allow_underfilled != 0;
+    if (a.constrained_rows) under = under && a.constrained_rows[row];
+    const bool enough = (greedy || under) ? real_count >= 1 : real_count >= top_k;
+
+    float sorted[1] = {sc.sel_score[lane]};
+    const int64_t sel_id = sc.sel_id[lane];
+    float retained[1], mass;
+    probabilities<1, false>(sorted, temperature, top_k, top_p, kWave, lane, retained, mass);
+    const int64_t random_seed = seed ^ (seed >> 32) ^ (ordinal >> 32);
+    const float uniform = philox_uniform2((uint32_t)random_seed, (uint32_t)((uint64_t)random_seed >> 32),
+                                          (uint32_t)ordinal);
+    const float target = uniform * mass;
+    vl_scan<1>(retained, kWave, lane);
+    const uint64_t hit = __ballot(retained[0] > target);
+    const int sampled = hit ? __builtin_ctzll(hit) : kWave;
+    const int chosen = greedy ? 0 : sampled;
+    const int64_t token = __shfl(sel_id, chosen & (kWave - 1));
+    const bool valid = malformed == 0 && params_ok && enough &&
+                       (greedy || (mass > 0.0f && sampled < kWave));
+    if (lane == 0) {
+        a.output_tokens[row] = valid ? token : -1;
+        a.output_valid[row] = valid ? 1 : 0;
+    }
 }
 
 // --------------------------------------------------------------------------
@@ -952,6 +1058,12 @@ hipError_t launch_verify(const VerifyArgs& a, hipStream_t s) {
     else if (a.block <= 128) verify_candidates_kernel<2><<<grid, block, 0, s>>>(a);
     else if (a.block <= 256) verify_candidates_kernel<4><<<grid, block, 0, s>>>(a);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_root_sample(const RootSampleArgs& a, hipStream_t s) {
+    if (a.tp * a.k > kRootThreads || a.k > kWave) return hipErrorInvalidValue;
+    root_sample_kernel<<<a.rows, kRootThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -451,6 +451,39 @@ int cubic_verify_candidates(const void* q_scores, const int64_t* q_ids, const vo
     return hip_status(cubic::launch_verify(a, (hipStream_t)stream), "cubic_verify_candidates launch");
 }
 
+int cubic_root_sample(const void* scores, int scores_fp16, const int64_t* ids,
+                      const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                      const int64_t* seeds, const int64_t* ordinals,
+                      const uint8_t* constrained_rows, int allow_underfilled, int tp, int rows,
+                      int k, int64_t* output_tokens, uint8_t* output_valid, void* stream) {
+    if (!scores || !ids || !temperatures || !top_ps || !top_ks || !seeds || !ordinals ||
+        !output_tokens || !output_valid)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (tp < 1 || tp > 8 || k < 1 || k > 20)
+        return fail(CUBIC_EINVAL, "scores must be [TP,C,K] with TP<=8 and K<=20");
+    if (rows < 1) return fail(CUBIC_EINVAL, "root sampling needs at least one row");
+    if (constrained_rows && !allow_underfilled)
+        return fail(CUBIC_EINVAL, "invalid constrained-row ownership for root sampling");
+    cubic::RootSampleArgs a = {};
+    a.scores = (const uint16_t*)scores;
+    a.scores_fp16 = scores_fp16 != 0;
+    a.ids = ids;
+    a.temperatures = temperatures;
+    a.top_ps = top_ps;
+    a.top_ks = top_ks;
+    a.seeds = seeds;
+    a.ordinals = ordinals;
+    a.constrained_rows = constrained_rows;
+    a.allow_underfilled = allow_underfilled != 0;
+    a.tp = tp;
+    a.rows = rows;
+    a.k = k;
+    a.block = next_pow2(tp * k);
+    a.output_tokens = output_tokens;
+    a.output_valid = output_valid;
+    return hip_status(cubic::launch_root_sample(a, (hipStream_t)stream), "cubic_root_sample launch");
+}
+
 int cubic_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
                        int live_rows, int64_t* out, void* stream) {
     if (!decisions || !out) return fail(CUBIC_EINVAL, "null operand");

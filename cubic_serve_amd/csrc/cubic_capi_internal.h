@@ -58,6 +58,22 @@ struct VerifyArgs {
     int tp, q_rows, p_rows, k, block, active_rows, allow_underfilled;
 };
 
+struct RootSampleArgs {
+    const uint16_t* scores;          // [tp, rows, k] bf16 or fp16
+    int scores_fp16;
+    const int64_t* ids;              // [tp, rows, k]
+    const float* temperatures;       // [rows]
+    const float* top_ps;
+    const int64_t* top_ks;
+    const int64_t* seeds;
+    const int64_t* ordinals;
+    const uint8_t* constrained_rows;  // [rows] bool or null
+    int allow_underfilled;
+    int tp, rows, k, block;          // block = next_pow2(tp * k)
+    int64_t* output_tokens;          // [rows]
+    uint8_t* output_valid;           // [rows] bool
+};
+
 struct GemmArgs {
     const uint16_t* x;            // [m, k] bf16, row stride ldx
     const uint32_t* codes;        // prepared code tiles
@@ -105,6 +121,7 @@ struct EmbedArgs {
 
 hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
+hipError_t launch_root_sample(const RootSampleArgs& a, hipStream_t s);
 hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
                                int live_rows, int64_t* out, hipStream_t s);
 hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t* a,

@@ -115,8 +115,9 @@ __device__ __forceinline__ float accept_expf(float x) {
 // counter (ordinal, 0, 0, 0) and key (key, 0), mapped to [0, 1) the way
 // tl.rand does: int32 bit pattern, negative x -> -x-1, times 2^-31 (rounded
 // constant 4.6566127342e-10).
-__device__ __forceinline__ float philox_uniform(uint32_t key, uint32_t ordinal) {
-    uint32_t c0 = ordinal, c1 = 0, c2 = 0, c3 = 0, k0 = key, k1 = 0;
+// Two-word key (k0, k1) = (low, high) 32 bits of tl.rand's 64-bit seed.
+__device__ __forceinline__ float philox_uniform2(uint32_t key_lo, uint32_t key_hi, uint32_t ordinal) {
+    uint32_t c0 = ordinal, c1 = 0, c2 = 0, c3 = 0, k0 = key_lo, k1 = key_hi;
 #pragma unroll
     for (int i = 0; i < 10; ++i) {
         const uint64_t a = (uint64_t)0xD2511F53u * c0, b = (uint64_t)0xCD9E8D57u * c2;
@@ -131,6 +132,10 @@ __device__ __forceinline__ float philox_uniform(uint32_t key, uint32_t ordinal) 
     int64_t sv = (int32_t)c0;
     if (sv < 0) sv = -sv - 1;
     return (float)sv * 4.6566127342e-10f;
+}
+
+__device__ __forceinline__ float philox_uniform(uint32_t key, uint32_t ordinal) {
+    return philox_uniform2(key, 0u, ordinal);
 }
 
 // Cross-workgroup hand-off without a full cache write-back: the producer

@@ -5,6 +5,7 @@ Host mirror of the reference's sampling API (paths under src/cubic_serve/):
   LocalCandidatePlan           ops/cuda/sampling/local_candidates.py:17-226
   ShardedSamplingWorkspace     generation/tp_sampling.py:57-64
   merge_prefix                 executor/draft_graph.py:146-157
+  RootTopKTopPSamplingPrimitive ops/cuda/sampling/topk_topp.py:124-278
   MTPVerifyPlan                the finish_review composition,
                                executor/draft_graph.py:1034-1067
 
@@ -102,6 +103,108 @@ def verify_one_draft_candidates(
             top_ps, top_ks, seeds, ordinals, uniforms, constrained_rows)),
             int(allow_underfilled), tp, q_rows, p_scores.shape[1], k, active_rows,
             decisions.data_ptr(), _native.stream_of(q_scores.device))
+
+
+_TensorABI = tuple
+
+
+def _abi(tensor: Tensor) -> _TensorABI:
+    if not isinstance(tensor, Tensor):
+        raise TypeError("sampling operands must be tensors")
+    return tuple(tensor.shape), tensor.stride(), tensor.dtype, tensor.device
+
+
+def _next_power_of_2(n: int) -> int:
+    return 1 << (n - 1).bit_length()
+
+
+@dataclass(frozen=True, slots=True)
+class RootTopKTopPSamplingMeta:
+    """Complete fixed launch identity for gathered ``[TP,C,K]`` candidates."""
+
+    device: torch.device
+    tp: int
+    rows: int
+    candidates_per_rank: int
+    block: int
+
+
+class RootTopKTopPSamplingPrimitive:
+    """Sample root-owned TP candidates without allocations or host RNG state.
+
+    Same constructor, ``launch`` and validation as topk_topp.py:141-278; the
+    launch is cubic_root_sample (one wave per row).
+    """
+
+    def __init__(self, scores: Tensor, token_ids: Tensor, temperatures: Tensor, top_ps: Tensor,
+                 top_ks: Tensor, seeds: Tensor, ordinals: Tensor, output_tokens: Tensor,
+                 output_valid: Tensor, *, allow_underfilled: bool = False,
+                 constrained_rows: Tensor | None = None) -> None:
+        if type(allow_underfilled) is not bool:
+            raise TypeError("candidate underfill policy must be boolean")
+        self.allow_underfilled = allow_underfilled
+        self._constraint_abi = None if constrained_rows is None else _abi(constrained_rows)
+        operands = (scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals,
+                    output_tokens, output_valid)
+        self._validate(operands)
+        if constrained_rows is not None and (
+                not allow_underfilled or constrained_rows.dtype != torch.bool
+                or constrained_rows.shape != temperatures.shape
+                or constrained_rows.device != temperatures.device
+                or not constrained_rows.is_contiguous()):
+            raise ValueError("invalid constrained-row ownership for root sampling")
+        tp, rows, k = scores.shape
+        self._abis = tuple(_abi(t) for t in operands)
+        self.meta = RootTopKTopPSamplingMeta(device=scores.device, tp=tp, rows=rows,
+                                             candidates_per_rank=k, block=_next_power_of_2(tp * k))
+
+    @property
+    def launch_signature(self) -> str:
+        m = self.meta
+        return (f"tp={m.tp},rows={m.rows},k={m.candidates_per_rank},block={m.block},"
+                f"scores=bf16,prob=fp32,rng=philox,allow_underfilled={int(self.allow_underfilled)}")
+
+    def launch(self, scores: Tensor, token_ids: Tensor, temperatures: Tensor, top_ps: Tensor,
+               top_ks: Tensor, seeds: Tensor, ordinals: Tensor, output_tokens: Tensor,
+               output_valid: Tensor, *, constrained_rows: Tensor | None = None) -> None:
+        """Enqueue one fixed-shape launch on the current stream."""
+        operands = (scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals,
+                    output_tokens, output_valid)
+        if tuple(_abi(t) for t in operands) != self._abis:
+            raise ValueError("sampling operands do not match the fixed launch ABI")
+        if (None if constrained_rows is None else _abi(constrained_rows)) != self._constraint_abi:
+            raise ValueError("constrained-row ownership differs from the fixed launch ABI")
+        m = self.meta
+        with torch.cuda.device(m.device):
+            _native.call("cubic_root_sample", scores.data_ptr(), int(scores.dtype == torch.float16),
+                         token_ids.data_ptr(), temperatures.data_ptr(), top_ps.data_ptr(),
+                         top_ks.data_ptr(), seeds.data_ptr(), ordinals.data_ptr(),
+                         _native.ptr(constrained_rows), int(self.allow_underfilled), m.tp, m.rows,
+                         m.candidates_per_rank, output_tokens.data_ptr(), output_valid.data_ptr(),
+                         _native.stream_of(m.device))
+
+    @staticmethod
+    def _validate(operands: tuple) -> None:
+        if any(not isinstance(t, Tensor) for t in operands):
+            raise TypeError("sampling operands must be tensors")
+        scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals, tokens, valid = operands
+        if any(t.device.type != "cuda" or not t.is_contiguous() for t in operands):
+            raise ValueError("all sampling operands must be contiguous CUDA tensors")
+        if len({t.device for t in operands}) != 1:
+            raise ValueError("all sampling operands must share one CUDA device")
+        if scores.ndim != 3 or not (1 <= scores.shape[0] <= 8) or not (1 <= scores.shape[2] <= 20):
+            raise ValueError("scores must be FP16/BF16 [TP,C,K] with TP<=8 and K<=20")
+        row_shape = (scores.shape[1],)
+        if (scores.shape[1] <= 0
+                or scores.dtype not in (torch.bfloat16, torch.float16)
+                or token_ids.dtype is not torch.int64 or token_ids.shape != scores.shape
+                or temperatures.dtype is not torch.float32 or top_ps.dtype is not torch.float32
+                or top_ks.dtype is not torch.int64 or seeds.dtype is not torch.int64
+                or ordinals.dtype is not torch.int64 or tokens.dtype is not torch.int64
+                or valid.dtype is not torch.bool
+                or any(t.shape != row_shape for t in operands[2:])):
+            raise ValueError("expected FP16/BF16 scores/int64 ids [TP,C,K], FP32 temperature/top_p, "
+                             "int64 top_k/seed/ordinal/token, and bool valid [C]")
 
 
 def merge_prefix(decisions: Tensor, out: Tensor, live: Tensor | int) -> None:

@@ -126,6 +126,28 @@ CUBIC_API int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, 
                              void* y, int64_t ldy, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Root top-k/top-p sampling of gathered [tp, rows, k] candidates (non-
+ * speculative decode).  Replaces RootTopKTopPSamplingPrimitive.launch and
+ * _root_topk_topp_kernel (ops/cuda/sampling/topk_topp.py:22-121, :141-278):
+ *   scores       bf16 (scores_fp16 = 0) or fp16 [tp, rows, k]; ids int64
+ *   temperatures/top_ps f32 [rows]; top_ks/seeds/ordinals int64 [rows]
+ *   constrained_rows bool [rows] or NULL (needs allow_underfilled)
+ *   output_tokens int64 [rows] (-1 when invalid), output_valid bool [rows]
+ * Global top-k (duplicate (score, id) pairs count once, ties by ascending
+ * id), temperature, softmax, top-p over the exclusive CDF, then the first
+ * candidate whose retained CDF exceeds u * retained mass, u = Philox4x32-10
+ * with key seed ^ (seed >> 32) ^ (ordinal >> 32) (both words) and counter
+ * (uint32) ordinal.  Greedy rows (temperature 0) take the top candidate.
+ * 1 <= tp <= 8, 1 <= k <= 20.  Reduction orders and exp as cubic_verify_candidates.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_root_sample(const void* scores, int scores_fp16, const int64_t* ids,
+                                const float* temperatures, const float* top_ps,
+                                const int64_t* top_ks, const int64_t* seeds,
+                                const int64_t* ordinals, const uint8_t* constrained_rows,
+                                int allow_underfilled, int tp, int rows, int k,
+                                int64_t* output_tokens, uint8_t* output_valid, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Packed embedding lookup: out[t, :] = decode(W[ids[t], :]) rounded to the
  * output dtype.  Replaces PackedLinearOperators.bind_embedding for Cubic
  * matrices (ops/cuda/linear/quantized.py:786-846) and the Cubic hook

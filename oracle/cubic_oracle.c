@@ -392,10 +392,11 @@ static void ks_scan(const float* in, int lanes, float* out) {
     for (int l = 0; l < lanes; ++l) out[l] = x[l];
 }
 
-static void probabilities(const float* scores, float temperature, int64_t top_k, float top_p,
-                          int lanes, float* out, float* mass_out) {
-    /* speculative.py:32-43 */
-    float logits[MAX_LANES] = {0}, w[MAX_LANES] = {0}, p[MAX_LANES] = {0}, incl[MAX_LANES] = {0};
+/* speculative.py:32-43 up to the retained mass; topk_topp.py:89-100 samples
+ * from these retained (not renormalised) probabilities. */
+static void retained_probabilities(const float* scores, float temperature, int64_t top_k,
+                                   float top_p, int lanes, float* p, float* mass_out) {
+    float logits[MAX_LANES] = {0}, w[MAX_LANES] = {0}, incl[MAX_LANES] = {0};
     const float safe_t = temperature == 0.0f ? 1.0f : temperature;
     float mx = -INFINITY; /* NaN-ignoring maximum, as Triton's tl.max */
     for (int l = 0; l < lanes; ++l) {
@@ -410,9 +411,15 @@ static void probabilities(const float* scores, float temperature, int64_t top_k,
         const float excl = incl[l] - p[l];
         p[l] = (l < top_k && excl <= top_p) ? p[l] : 0.0f;
     }
-    const float mass = tree_sum(p, lanes);
-    for (int l = 0; l < lanes; ++l) out[l] = p[l] / mass;
-    *mass_out = mass;
+    *mass_out = tree_sum(p, lanes);
+}
+
+static void probabilities(const float* scores, float temperature, int64_t top_k, float top_p,
+                          int lanes, float* out, float* mass_out) {
+    /* speculative.py:32-43 */
+    float p[MAX_LANES] = {0};
+    retained_probabilities(scores, temperature, top_k, top_p, lanes, p, mass_out);
+    for (int l = 0; l < lanes; ++l) out[l] = p[l] / *mass_out;
 }
 
 static int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
@@ -523,6 +530,69 @@ EXPORT int oracle_verify_k1(const uint16_t* q_scores, const int64_t* q_ids,
         const int64_t next = greedy ? greedy_next : (accepted ? p1_token : res_token);
         decisions[row * 2] = valid ? (int64_t)accepted : -1;
         decisions[row * 2 + 1] = valid ? next : -1;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* F2  _root_topk_topp_kernel -- ops/cuda/sampling/topk_topp.py:22-121,      */
+/* lane by lane over BLOCK = next_pow2(TP*K) lanes, with the reduction      */
+/* orders and exp of A14.  `uniforms` (test hook, may be NULL) replaces the */
+/* Philox draw per row, as the reference test oracle makes it explicit       */
+/* (tests/ops/test_cuda_topk_topp_sampling.py:16-62).                       */
+/* ------------------------------------------------------------------------ */
+EXPORT int oracle_root_sample(const uint16_t* scores, int scores_fp16, const int64_t* ids,
+                              const float* temperatures, const float* top_ps,
+                              const int64_t* top_ks, const int64_t* seeds,
+                              const int64_t* ordinals, const float* uniforms,
+                              const uint8_t* constrained_rows, int allow_underfilled, int tp,
+                              int rows, int k, int64_t* out_tokens, uint8_t* out_valid) {
+    const int lanes = next_pow2(tp * k);
+    if (lanes > MAX_LANES) return -1;
+    for (int row = 0; row < rows; ++row) {
+        float sc[MAX_LANES];
+        int64_t id[MAX_LANES];
+        int real[MAX_LANES];
+        int pairs_valid = 1;
+        for (int l = 0; l < lanes; ++l) {
+            const int cm = l < tp * k;
+            const int64_t off = ((int64_t)(l / k) * rows + row) * k + l % k;
+            const uint16_t b = cm ? scores[off] : 0;
+            sc[l] = !cm ? -INFINITY : scores_fp16 ? oracle_half_to_float(b) : oracle_bf16_to_float(b);
+            id[l] = cm ? ids[off] : -1;
+            real[l] = cm && isfinite(sc[l]) && id[l] >= 0;
+            const int sentinel = cm && sc[l] != sc[l] && id[l] == -1;
+            if (cm && !real[l] && !sentinel) pairs_valid = 0;
+        }
+        float ss[MAX_LANES];
+        int64_t si[MAX_LANES];
+        int real_count;
+        select_topk(sc, id, real, lanes, k, ss, si, &real_count);
+        const float temperature = temperatures[row], top_p = top_ps[row];
+        const int64_t top_k = top_ks[row], seed = seeds[row], ordinal = ordinals[row];
+        const int greedy = temperature == 0.0f;
+        const int params_ok = temperature == temperature && temperature >= 0.0f &&
+                              temperature < INFINITY && top_p == top_p && top_p > 0.0f &&
+                              top_p <= 1.0f && top_k >= 1 && top_k <= k && seed >= 0 && ordinal >= 0;
+        int underfilled = allow_underfilled;
+        if (constrained_rows) underfilled = underfilled && constrained_rows[row];
+        const int enough = (greedy || underfilled) ? real_count >= 1 : real_count >= top_k;
+        float retained[MAX_LANES] = {0}, cdf[MAX_LANES], mass;
+        retained_probabilities(ss, temperature, top_k, top_p, lanes, retained, &mass);
+        const int64_t random_seed = seed ^ (seed >> 32) ^ (ordinal >> 32);
+        const float u = uniforms ? uniforms[row]
+                                 : oracle_philox_uniform((uint64_t)random_seed, (uint32_t)ordinal);
+        const float target = u * mass;
+        ks_scan(retained, lanes, cdf);
+        int sampled = lanes;
+        for (int l = 0; l < lanes; ++l)
+            if (cdf[l] > target) { sampled = l; break; }
+        const int chosen = greedy ? 0 : sampled;
+        const int64_t token = chosen < lanes ? si[chosen] : INT64_MAXV;
+        const int valid = pairs_valid && params_ok && enough &&
+                          (greedy || (mass > 0.0f && sampled < lanes));
+        out_tokens[row] = valid ? token : -1;
+        out_valid[row] = (uint8_t)valid;
     }
     return 0;
 }

@@ -16,6 +16,7 @@ linear_bf16               ops/eager/linear.py:43-56 + quantization.py:181  FP64 
 check_linear_enclosure    guardrail/quantization.py:176-320                 closed form; rejects a +0.25 corruption
 candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows
 verify_k1                 ops/cuda/sampling/speculative.py:46-219           reference KATs :73-131, :230-309; frozen-draw sweep :133-228; double-precision _oracle
+root_sample               ops/cuda/sampling/topk_topp.py:22-121             reference oracle KATs tests/ops/test_cuda_topk_topp_sampling.py:65-91 and CUDA-test expectations :127-201; float64 brute force with explicit uniforms
 merge_prefix              executor/draft_graph.py:146-157                   chain KATs tests/generation/test_tp_sampling.py:120-178
 philox_uniform            guardrail/quantized_graph/speculative.py:15-30    Random123 Philox4x32-10 known-answer vectors
 expf                      (build-fixed exp for the acceptance transform)    <= 2 ulp against libm expf over a dense sweep
@@ -276,6 +277,27 @@ def verify_k1(q_scores, q_ids, p_scores, p_ids, target_rows, draft_tokens, tempe
     if rc:
         raise ValueError("candidate block too wide")
     return dec
+
+
+def root_sample(scores, ids, temperatures, top_ps, top_ks, seeds, ordinals, *, fp16=False,
+                uniforms=None, allow_underfilled=False, constrained_rows=None):
+    """(tokens int64 [C], valid bool [C]) for fp16/bf16-bit candidates [TP, C, K]
+    (ops/cuda/sampling/topk_topp.py:22-121).  ``uniforms`` [C] replaces the
+    Philox draw (test hook, as the reference test oracle does)."""
+    scores, ids = _c(scores, np.uint16), _c(ids, np.int64)
+    tp, rows, k = scores.shape
+    tokens = np.empty(rows, np.int64)
+    valid = np.empty(rows, np.uint8)
+    uni = None if uniforms is None else _c(uniforms, np.float32)
+    con = None if constrained_rows is None else _c(constrained_rows, np.uint8)
+    rc = lib().oracle_root_sample(
+        _p(scores), ctypes.c_int(int(fp16)), _p(ids), _p(_c(temperatures, np.float32)),
+        _p(_c(top_ps, np.float32)), _p(_c(top_ks, np.int64)), _p(_c(seeds, np.int64)),
+        _p(_c(ordinals, np.int64)), _p(uni), _p(con), ctypes.c_int(int(allow_underfilled)),
+        ctypes.c_int(tp), ctypes.c_int(rows), ctypes.c_int(k), _p(tokens), _p(valid))
+    if rc:
+        raise ValueError("candidate block too wide")
+    return tokens, valid.astype(bool)
 
 
 def merge_prefix(decisions: np.ndarray, live_rows: int) -> np.ndarray:

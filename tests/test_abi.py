@@ -60,3 +60,26 @@ def test_invalid_arguments_fail_before_any_launch():
     with pytest.raises(ValueError, match="group_out"):
         _native.call("cubic_embedding", 16, 8, 4, 0, 16, 16, 16, 16, None, None, None, None,
                      64, 128, 4, 32, 3, 16, 0, None)
+    with pytest.raises(ValueError, match="TP<=8"):
+        _native.call("cubic_root_sample", 16, 0, 16, 16, 16, 16, 16, 16, None, 0, 9, 4, 20, 16, 16, None)
+    with pytest.raises(ValueError, match="constrained-row"):
+        _native.call("cubic_root_sample", 16, 0, 16, 16, 16, 16, 16, 16, 16, 0, 4, 4, 20, 16, 16, None)
+
+
+def test_root_sampler_rejects_cpu_storage():
+    import torch
+
+    from cubic_serve_amd import sampling
+
+    scores = torch.empty((4, 1, 20), dtype=torch.bfloat16)
+    rows = lambda dtype: torch.empty((1,), dtype=dtype)
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        sampling.RootTopKTopPSamplingPrimitive(
+            scores, torch.empty_like(scores, dtype=torch.int64), rows(torch.float32),
+            rows(torch.float32), rows(torch.int64), rows(torch.int64), rows(torch.int64),
+            rows(torch.int64), rows(torch.bool))
+    with pytest.raises(TypeError, match="boolean"):
+        sampling.RootTopKTopPSamplingPrimitive(
+            scores, torch.empty_like(scores, dtype=torch.int64), rows(torch.float32),
+            rows(torch.float32), rows(torch.int64), rows(torch.int64), rows(torch.int64),
+            rows(torch.int64), rows(torch.bool), allow_underfilled=1)
