@@ -222,7 +222,8 @@ def measure_extras() -> dict:
     acceptance of batch 64 x k = 3 (T 0.7, top-p 0.9, top-k 20, seeded
     uniforms) over N(0, 3) target logits, q candidates from target + N(0, 1).
     cfg4: routed experts, 128 experts, top-8, hidden 2048, intermediate 768,
-    W4 g128, 256 tokens, router logits N(0, 1): gate/up and down launches.
+    W4 g128, 256 tokens, router logits N(0, 1): gate/up and down launches,
+    the router (top-8 of 128 + softmax) and the route compaction.
     embedding: packed lookup from a Qwen3-8B-shaped W4 g128 table (random
     payload) for 64 tokens (one verify step) and 16384 tokens (prefill).
     root_sampler: top-k/top-p sampling of TP=4 x K=20 candidates for 1 and
@@ -292,6 +293,11 @@ def measure_extras() -> dict:
     xd = torch.randn((tokens * top_k, inter), generator=g, device=dev).to(torch.bfloat16)
     yd = torch.empty((tokens * top_k, hidden), dtype=torch.bfloat16, device=dev)
     _, b2 = moe.bind_routed(ops, xd, down, yd, routed)
+    routing = moe.MoERouting(torch.randn((tokens, experts), generator=g, device=dev).to(torch.bfloat16),
+                             torch.ones(tokens, dtype=torch.int32, device=dev),
+                             torch.tensor([tokens], dtype=torch.int32, device=dev), top_k=top_k)
+    route_ms = time_graph(capture(lambda: [routing.select.launch() for _ in range(20)]), 10, 2) / 20
+    compact_ms = time_graph(capture(lambda: [routing.compact.launch() for _ in range(20)]), 10, 2) / 20
     gu_ms = time_graph(capture(b1.launch), 20, 3)
     dn_ms = time_graph(capture(b2.launch), 20, 3)
     routes = tokens * top_k
@@ -300,7 +306,8 @@ def measure_extras() -> dict:
     out["cfg4"] = {"gate_up_us": round(gu_ms * 1e3, 2), "gate_up_gbs": round(gu_bytes / gu_ms / 1e6, 1),
                    "down_us": round(dn_ms * 1e3, 2), "down_gbs": round(dn_bytes / dn_ms / 1e6, 1),
                    "layer_us": round((gu_ms + dn_ms) * 1e3, 2),
-                   "layer_gbs": round((gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e6, 1)}
+                   "layer_gbs": round((gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e6, 1),
+                   "router_us": round(route_ms * 1e3, 2), "compact_us": round(compact_ms * 1e3, 2)}
     del gate, up, down, b1, b2, h, xd, yd
     # ---- packed embedding (cfg2 model: Qwen3-8B table 151936 x 4096, W4 g128)
     groups = (VOCAB, HIDDEN // GROUP)

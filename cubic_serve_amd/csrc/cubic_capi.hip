@@ -254,6 +254,56 @@ int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const 
                        ldy1, workspace, workspace_bytes, stream);
 }
 
+int cubic_moe_route(const void* logits, int logits_fp16, const int32_t* row_activity,
+                    const int32_t* active_rows, int rows, int experts, int top_k, float* top_logits,
+                    int64_t* top_ids, int64_t* route_ids, void* route_weights, int weights_fp16,
+                    void* stream) {
+    if (!logits || !row_activity || !active_rows || !top_logits || !top_ids || !route_ids ||
+        !route_weights)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (rows < 1 || experts < 1 || experts > cubic::kMaxRouteExperts)
+        return fail(CUBIC_ENOTSUP, "router needs 1 <= experts <= %d", cubic::kMaxRouteExperts);
+    if (top_k < 1 || top_k > experts || top_k > cubic::kMaxRouteTopK)
+        return fail(CUBIC_EINVAL, "router needs a valid top-k (1..min(experts, %d))", cubic::kMaxRouteTopK);
+    cubic::MoERouteArgs a = {};
+    a.logits = (const uint16_t*)logits;
+    a.logits_fp16 = logits_fp16 != 0;
+    a.row_activity = row_activity;
+    a.active_rows = active_rows;
+    a.rows = rows;
+    a.experts = experts;
+    a.top_k = top_k;
+    a.top_logits = top_logits;
+    a.top_ids = top_ids;
+    a.route_ids = route_ids;
+    a.route_weights = (uint16_t*)route_weights;
+    a.weights_fp16 = weights_fp16 != 0;
+    return hip_status(cubic::launch_moe_route(a, (hipStream_t)stream), "cubic_moe_route launch");
+}
+
+int cubic_moe_compact(const int64_t* route_ids, int routes, int first_expert, int experts,
+                      int block_m, int32_t* counts, int32_t* starts, int32_t* block_starts,
+                      int32_t* total_blocks, int32_t* row_map, void* stream) {
+    if (!route_ids || !counts || !starts || !block_starts || !total_blocks || !row_map)
+        return fail(CUBIC_EINVAL, "null operand");
+    if (routes < 1 || first_expert < 0 || block_m < 1)
+        return fail(CUBIC_EINVAL, "compaction needs routes >= 1, first_expert >= 0, block_m >= 1");
+    if (experts < 1 || experts > cubic::kMaxCompactExperts)
+        return fail(CUBIC_ENOTSUP, "compaction needs 1 <= experts <= %d", cubic::kMaxCompactExperts);
+    cubic::MoECompactArgs a = {};
+    a.route_ids = route_ids;
+    a.routes = routes;
+    a.first_expert = first_expert;
+    a.experts = experts;
+    a.block_m = block_m;
+    a.counts = counts;
+    a.starts = starts;
+    a.block_starts = block_starts;
+    a.total_blocks = total_blocks;
+    a.row_map = row_map;
+    return hip_status(cubic::launch_moe_compact(a, (hipStream_t)stream), "cubic_moe_compact launch");
+}
+
 int cubic_embedding(const void* ids, int id_bytes, int64_t tokens, int fmt, const void* packed,
                     const void* m0, const void* m1, const void* m2, const void* g0, const void* g1,
                     const void* g2, const int32_t* part_of_row, int64_t n, int64_t k, int bits,

@@ -74,6 +74,35 @@ struct RootSampleArgs {
     uint8_t* output_valid;           // [rows] bool
 };
 
+// MoE router (cubic_moe.hip)
+constexpr int kMaxRouteExperts = 1024;
+constexpr int kMaxRouteTopK = 64;
+struct MoERouteArgs {
+    const uint16_t* logits;       // [rows, experts] bf16 or fp16
+    int logits_fp16;
+    const int32_t* row_activity;  // [rows]
+    const int32_t* active_rows;   // device scalar
+    int rows, experts, top_k;
+    float* top_logits;            // [rows, top_k] (logit desc order)
+    int64_t* top_ids;             // [rows, top_k]
+    int64_t* route_ids;           // [rows, top_k] ascending expert id
+    uint16_t* route_weights;      // [rows, top_k] bf16 or fp16
+    int weights_fp16;
+};
+
+// Route compaction (cubic_moe.hip)
+constexpr int kMaxCompactExperts = 1024;
+constexpr int kCompactExpertBits = 10;  // 2^bits >= kMaxCompactExperts
+struct MoECompactArgs {
+    const int64_t* route_ids;  // [routes] global expert ids (-1 / others unowned)
+    int routes, first_expert, experts, block_m;
+    int32_t* counts;           // [experts]
+    int32_t* starts;
+    int32_t* block_starts;
+    int32_t* total_blocks;     // [1]
+    int32_t* row_map;          // [routes]; only owned positions written
+};
+
 struct GemmArgs {
     const uint16_t* x;            // [m, k] bf16, row stride ldx
     const uint32_t* codes;        // prepared code tiles
@@ -140,6 +169,9 @@ hipError_t launch_expand_metadata(int fmt, const void* m0, const void* m1, const
                                   const int32_t* part_of_row,
                                   int64_t n, int64_t groups_k, int group_out, float* scale,
                                   uint16_t* a, uint16_t* b, hipStream_t s);
+
+hipError_t launch_moe_route(const MoERouteArgs& a, hipStream_t s);
+hipError_t launch_moe_compact(const MoECompactArgs& a, hipStream_t s);
 
 // Packed embedding lookup (quantization/extensions/cubic/linear.py:266-294)
 hipError_t launch_embedding(const EmbedArgs& a, hipStream_t s);

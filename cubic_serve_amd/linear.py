@@ -368,8 +368,6 @@ class PackedLinearOperators:
         """Bind a lookup; ids are read at launch (validation quantized.py:793-826)."""
         if not isinstance(weight, QuantizedMatrix) or len(weight.shape) != 2:
             raise ValueError("native Cubic embedding requires a packed matrix weight")
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("Cubic embeddings must be bound before graph capture")
         tensors = (input_ids, output, *weight.payload.values())
         k = weight.shape[1]
         if (not input_ids.is_cuda
@@ -381,6 +379,8 @@ class PackedLinearOperators:
             raise ValueError("bound embedding requires contiguous same-device IDs, weight and FP16/BF16 output")
         if any(_storage(output) == _storage(t) for t in (input_ids, *weight.payload.values())):
             raise ValueError("bound embedding output must not alias its operands")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("Cubic embeddings must be bound before graph capture")
         return bind_embedding(self, input_ids, weight, output, params)
 
     def linear(self, x: Tensor, weight: QuantizedMatrix) -> Tensor:

@@ -1,5 +1,9 @@
 """Routed-expert (MoE) Cubic GEMM behind the Cubic extension's MoE hooks.
 
+Router and compaction: ``bind_route_selection`` (ops/cuda/moe/quantized.py:58-180,
+kernels ops/cuda/moe/fused.py:44-156) and ``bind_compact_routes``
+(_compact_local_routes, fused.py:174-199), composed by ``MoERouting``.
+
 Mirrors quantization/extensions/cubic/marlin.py:84-253 (``bind_grouped`` for
 gate/up, ``bind_routed`` for down, both returning ``(block_m, binding)`` or
 None when not admitted) over ``RoutedRows`` (quantization/api.py:123-134).
@@ -53,26 +57,148 @@ class CubicMoEParameters:
     block_m: int = 32
 
 
-def route_rows(topk_ids: Tensor, experts: int, block_m: int) -> RoutedRows:
-    """Compact top-k routes by expert, stable in route ordinal.
+def _i32(n: int, device) -> Tensor:
+    return torch.empty((n,), dtype=torch.int32, device=device)
 
-    Tensor restatement of the compaction of ops/cuda/moe/fused.py:175-199
-    (histogram, exclusive prefix of counts and of blocks, route order by
-    (expert, ordinal)); used to feed the routed GEMM.
+
+class _RouteLaunch:
+    """cubic_moe_route over fixed operands (identity-checked at launch)."""
+
+    def __init__(self, *operands: Tensor):
+        self.operands = operands
+        self.identity = self._identity()
+
+    def _identity(self):
+        return tuple((t.data_ptr(), tuple(t.shape), t.dtype) for t in self.operands)
+
+    def validate(self) -> None:
+        if self._identity() != self.identity:
+            raise ValueError("routing operands changed after binding")
+
+    def __call__(self, stream: int) -> None:
+        logits, activity, active_rows, top_logits, top_ids, route_ids, route_weights = self.operands
+        rows, experts = logits.shape
+        _native.call("cubic_moe_route", logits.data_ptr(), int(logits.dtype == torch.float16),
+                     activity.data_ptr(), active_rows.data_ptr(), rows, experts, top_ids.shape[1],
+                     top_logits.data_ptr(), top_ids.data_ptr(), route_ids.data_ptr(),
+                     route_weights.data_ptr(), int(route_weights.dtype == torch.float16), stream)
+
+
+class _CompactLaunch(_RouteLaunch):
+    """cubic_moe_compact over fixed operands."""
+
+    def __init__(self, *operands: Tensor, first_expert: int, experts: int, block_m: int):
+        super().__init__(*operands)
+        self.first_expert, self.experts, self.block_m = first_expert, experts, block_m
+
+    def __call__(self, stream: int) -> None:
+        route_ids, counts, starts, block_starts, total, row_map = self.operands
+        _native.call("cubic_moe_compact", route_ids.data_ptr(), route_ids.numel(), self.first_expert,
+                     self.experts, self.block_m, counts.data_ptr(), starts.data_ptr(),
+                     block_starts.data_ptr(), total.data_ptr(), row_map.data_ptr(), stream)
+
+
+def bind_route_selection(logits: Tensor, activity: Tensor, active_rows: Tensor, top_logits: Tensor,
+                         top_ids: Tensor, route_ids: Tensor, route_weights: Tensor) -> PackedOperatorBinding:
+    """Router launch (ops/cuda/moe/quantized.py:58-180, kernels fused.py:44-156).
+
+    Per row: top_k experts by (logit desc, id asc) into top_logits/top_ids;
+    softmax over those logits, ordered by ascending expert id, into
+    route_ids/route_weights.  Rows at or past ``active_rows[0]`` or with
+    ``activity`` 0 publish 0 / -1 / -1 / 0.
+    """
+    tensors = (logits, activity, active_rows, top_logits, top_ids, route_ids, route_weights)
+    if any(not isinstance(t, Tensor) for t in tensors):
+        raise TypeError("routing operands must be tensors")
+    if any(t.device.type != "cuda" or t.device != logits.device or not t.is_contiguous() for t in tensors):
+        raise ValueError("routing operands must be contiguous tensors on one CUDA device")
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("routing must be bound before graph capture")
+    if logits.ndim != 2 or top_ids.ndim != 2:
+        raise ValueError("router needs [rows,experts] logits and [rows,top_k] outputs")
+    rows, experts = logits.shape
+    top_k = top_ids.shape[1]
+    if (logits.dtype not in (torch.bfloat16, torch.float16)
+            or activity.dtype is not torch.int32 or activity.shape != (rows,)
+            or active_rows.dtype is not torch.int32 or active_rows.shape != (1,)
+            or top_logits.dtype is not torch.float32 or top_logits.shape != (rows, top_k)
+            or top_ids.dtype is not torch.int64 or route_ids.dtype is not torch.int64
+            or route_ids.shape != (rows, top_k) or route_weights.shape != (rows, top_k)
+            or route_weights.dtype not in (torch.bfloat16, torch.float16)):
+        raise ValueError("routing operands differ from the BF16/FP16 router ABI")
+    if not 0 < top_k <= experts:
+        raise ValueError("router needs [rows,experts] logits and a valid top-k")
+    return PackedOperatorBinding(route_weights, (_RouteLaunch(*tensors),))
+
+
+def bind_compact_routes(route_ids: Tensor, counts: Tensor, starts: Tensor, block_starts: Tensor,
+                        total_blocks: Tensor, row_map: Tensor, *, first_expert: int, experts: int,
+                        block_m: int) -> PackedOperatorBinding:
+    """Compaction launch (_compact_local_routes, ops/cuda/moe/fused.py:174-199)."""
+    tensors = (route_ids, counts, starts, block_starts, total_blocks, row_map)
+    if any(t.device.type != "cuda" or t.device != route_ids.device or not t.is_contiguous()
+           for t in tensors):
+        raise ValueError("compaction operands must be contiguous tensors on one CUDA device")
+    if (route_ids.dtype is not torch.int64 or any(t.dtype is not torch.int32 for t in tensors[1:])
+            or any(t.shape != (experts,) for t in (counts, starts, block_starts))
+            or total_blocks.shape != (1,) or row_map.shape != (route_ids.numel(),)):
+        raise ValueError("compaction operands differ from the route ABI")
+    if type(first_expert) is not int or first_expert < 0 or type(block_m) is not int or block_m < 1:
+        raise ValueError("compaction needs first_expert >= 0 and block_m >= 1")
+    return PackedOperatorBinding(row_map, (_CompactLaunch(*tensors, first_expert=first_expert,
+                                                          experts=experts, block_m=block_m),))
+
+
+def route_rows(topk_ids: Tensor, experts: int, block_m: int, first_expert: int = 0) -> RoutedRows:
+    """Compact [tokens, top_k] routes by expert on the device (allocates).
+
+    Routes outside [first_expert, first_expert + experts) are skipped; the
+    row map then holds only the owned routes (the rest of it is unspecified).
     """
     if topk_ids.ndim != 2:
         raise ValueError("routes need [tokens, top_k] expert ids")
-    ids = topk_ids.reshape(-1).to(torch.int64)
-    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= experts):
-        raise ValueError("expert id out of range")
-    routes = ids.numel()
-    order = torch.argsort(ids * max(routes, 1) + torch.arange(routes, device=ids.device))
-    counts = torch.bincount(ids, minlength=experts)
-    blocks = (counts + block_m - 1) // block_m
-    i32 = lambda t: t.to(torch.int32).contiguous()
-    return RoutedRows(i32(counts), i32(torch.cumsum(counts, 0) - counts),
-                      i32(torch.cumsum(blocks, 0) - blocks), i32(blocks.sum().reshape(1)), i32(order),
-                      mean_rows_per_expert=routes / experts, routing_top_k=topk_ids.shape[1])
+    ids = topk_ids.to(torch.int64).contiguous()
+    dev = ids.device
+    rows = RoutedRows(_i32(experts, dev), _i32(experts, dev), _i32(experts, dev), _i32(1, dev),
+                      _i32(ids.numel(), dev), mean_rows_per_expert=ids.numel() / experts,
+                      routing_top_k=topk_ids.shape[1])
+    bind_compact_routes(ids, rows.counts, rows.starts, rows.block_starts, rows.total_blocks,
+                        rows.row_map, first_expert=first_expert, experts=experts,
+                        block_m=block_m).launch()
+    return rows
+
+
+class MoERouting:
+    """Router + compaction for fixed [rows, experts] logits (bound once).
+
+    ``launch()`` enqueues the router then the compaction; afterwards
+    ``route_ids``/``route_weights`` hold the routes and ``rows`` the
+    expert-grouped RoutedRows that bind_grouped / bind_routed consume.
+    """
+
+    def __init__(self, logits: Tensor, activity: Tensor, active_rows: Tensor, *, top_k: int,
+                 first_expert: int = 0, experts: int | None = None, block_m: int = 32,
+                 weights_dtype: torch.dtype | None = None):
+        dev = logits.device
+        m, global_experts = logits.shape
+        experts = global_experts - first_expert if experts is None else experts
+        self.top_logits = torch.empty((m, top_k), dtype=torch.float32, device=dev)
+        self.top_ids = torch.empty((m, top_k), dtype=torch.int64, device=dev)
+        self.route_ids = torch.empty_like(self.top_ids)
+        self.route_weights = torch.empty((m, top_k), dtype=weights_dtype or logits.dtype, device=dev)
+        self.rows = RoutedRows(_i32(experts, dev), _i32(experts, dev), _i32(experts, dev), _i32(1, dev),
+                               _i32(m * top_k, dev), mean_rows_per_expert=m * top_k / experts,
+                               routing_top_k=top_k)
+        self.select = bind_route_selection(logits, activity, active_rows, self.top_logits, self.top_ids,
+                                           self.route_ids, self.route_weights)
+        r = self.rows
+        self.compact = bind_compact_routes(self.route_ids, r.counts, r.starts, r.block_starts,
+                                           r.total_blocks, r.row_map, first_expert=first_expert,
+                                           experts=experts, block_m=block_m)
+
+    def launch(self) -> None:
+        self.select.launch()
+        self.compact.launch()
 
 
 @dataclass(frozen=True, slots=True)

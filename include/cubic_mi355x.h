@@ -171,6 +171,38 @@ CUBIC_API int cubic_embedding(const void* ids, int id_bytes, int64_t tokens, int
                               int group_in, int group_out, void* out, int out_dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * MoE router: per row, the top_k experts by (logit desc, expert id asc), then
+ * a softmax over the selected logits, re-ordered by ascending expert id.
+ * Replaces the routing launches of PackedRoutedExpertsPrimitive
+ * (_bind_route_selection, ops/cuda/moe/quantized.py:58-180, kernels
+ * _stable_topk_logits + _sort_and_normalize_topk / _stable_topk_routes,
+ * ops/cuda/moe/fused.py:44-156):
+ *   logits        bf16 / fp16 [rows, experts] (logits_fp16)
+ *   row_activity  int32 [rows]; active_rows int32 device scalar: rows at or
+ *                 past it, or with activity 0, publish 0 / -1 / -1 / 0
+ *   top_logits f32, top_ids int64 [rows, top_k] in (logit desc) order
+ *   route_ids int64, route_weights bf16 / fp16 (weights_fp16) [rows, top_k]
+ *   in ascending expert order
+ * 1 <= experts <= 1024, 1 <= top_k <= min(experts, 64).  exp and the sum
+ * order are build-defined (as cubic_verify_candidates); logits must be finite.
+ *
+ * cubic_moe_compact: routes of experts [first_expert, first_expert + experts)
+ * grouped by expert, ascending route ordinal inside each expert; counts,
+ * starts, block starts (blocks of block_m) and the total block count
+ * (_compact_local_routes, ops/cuda/moe/fused.py:174-199).  Other routes are
+ * skipped; row_map positions past the owned routes are not written.
+ * 1 <= experts <= 1024.  The outputs feed cubic_moe_pad_routes.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_moe_route(const void* logits, int logits_fp16, const int32_t* row_activity,
+                              const int32_t* active_rows, int rows, int experts, int top_k,
+                              float* top_logits, int64_t* top_ids, int64_t* route_ids,
+                              void* route_weights, int weights_fp16, void* stream);
+CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_expert,
+                                int experts, int block_m, int32_t* counts, int32_t* starts,
+                                int32_t* block_starts, int32_t* total_blocks, int32_t* row_map,
+                                void* stream);
+
+/* ---------------------------------------------------------------------------
  * Candidate preparation: vocab logits -> top-`count` candidates per row.
  * Replaces LocalCandidatePlan.launch (ops/cuda/sampling/local_candidates.py:
  * 206-226: torch.topk + candidate_partial/candidate_publish,

@@ -598,6 +598,78 @@ EXPORT int oracle_root_sample(const uint16_t* scores, int scores_fp16, const int
 }
 
 /* ------------------------------------------------------------------------ */
+/* F4  MoE router -- ops/cuda/moe/fused.py:44-100 (_stable_topk_logits then */
+/* _sort_and_normalize_topk; the fused _stable_topk_routes :103-156 gives   */
+/* the same bits).  K rounds of (max logit, lowest expert among equals);    */
+/* softmax over the selected logits with the build's exp and a butterfly    */
+/* sum over next_pow2(K) lanes; ids re-ordered ascending.                   */
+/* ------------------------------------------------------------------------ */
+EXPORT int oracle_moe_route(const uint16_t* logits, int logits_fp16, const int32_t* activity,
+                            int active_rows, int rows, int experts, int top_k, float* top_logits,
+                            int64_t* top_ids, int64_t* route_ids, uint16_t* route_weights,
+                            int weights_fp16) {
+    if (top_k < 1 || top_k > experts || top_k > MAX_LANES) return -1;
+    float* v = (float*)malloc(sizeof(float) * (size_t)experts);
+    int* taken = (int*)malloc(sizeof(int) * (size_t)experts);
+    if (!v || !taken) { free(v); free(taken); return -2; }
+    const int lanes = next_pow2(top_k);
+    for (int r = 0; r < rows; ++r) {
+        const int active = r < active_rows && activity[r] > 0;
+        for (int e = 0; e < experts; ++e) {
+            const uint16_t b = logits[(int64_t)r * experts + e];
+            v[e] = logits_fp16 ? oracle_half_to_float(b) : oracle_bf16_to_float(b);
+            taken[e] = 0;
+        }
+        float sc[MAX_LANES];
+        int64_t id[MAX_LANES];
+        for (int i = 0; i < top_k; ++i) {
+            int best = -1;
+            for (int e = 0; e < experts; ++e)
+                if (!taken[e] && (best < 0 || v[e] > v[best])) best = e;  /* first = lowest id on ties */
+            taken[best] = 1;
+            sc[i] = v[best];
+            id[i] = best;
+            top_logits[(int64_t)r * top_k + i] = active ? v[best] : 0.0f;
+            top_ids[(int64_t)r * top_k + i] = active ? best : -1;
+        }
+        float mx = -INFINITY, p[MAX_LANES];
+        for (int i = 0; i < top_k; ++i) if (sc[i] > mx) mx = sc[i];
+        for (int l = 0; l < lanes; ++l) p[l] = l < top_k ? oracle_expf(sc[l] - mx) : 0.0f;
+        const float den = tree_sum(p, lanes);
+        for (int i = 0; i < top_k; ++i) {
+            int out = 0;
+            for (int j = 0; j < top_k; ++j) out += id[j] < id[i];
+            const float w = p[i] / den;
+            route_ids[(int64_t)r * top_k + out] = active ? id[i] : -1;
+            route_weights[(int64_t)r * top_k + out] =
+                !active ? 0 : weights_fp16 ? oracle_float_to_half(w) : oracle_float_to_bf16(w);
+        }
+    }
+    free(v);
+    free(taken);
+    return 0;
+}
+
+/* F4  route compaction -- ops/cuda/moe/fused.py:174-199 (_compact_local_routes). */
+EXPORT int oracle_moe_compact(const int64_t* route_ids, int routes, int first_expert, int experts,
+                              int block_m, int32_t* counts, int32_t* starts, int32_t* block_starts,
+                              int32_t* total_blocks, int32_t* row_map) {
+    int32_t c = 0, b = 0;
+    for (int e = 0; e < experts; ++e) {
+        int32_t n = 0;
+        for (int r = 0; r < routes; ++r) n += route_ids[r] - first_expert == e;
+        counts[e] = n;
+        starts[e] = c;
+        block_starts[e] = b;
+        for (int r = 0; r < routes; ++r)
+            if (route_ids[r] - first_expert == e) row_map[c++] = r;
+        b += (n + block_m - 1) / block_m;
+    }
+    *total_blocks = b;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* A15  merge_prefix -- executor/draft_graph.py:146-157.                     */
 /* decisions [depth, c, 2] -> out [c, 2]: accepted = first depth whose      */
 /* accept flag is 0 (else depth); bonus = that depth's next token (else the */

@@ -17,6 +17,8 @@ check_linear_enclosure    guardrail/quantization.py:176-320                 clos
 candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows
 verify_k1                 ops/cuda/sampling/speculative.py:46-219           reference KATs :73-131, :230-309; frozen-draw sweep :133-228; double-precision _oracle
 root_sample               ops/cuda/sampling/topk_topp.py:22-121             reference oracle KATs tests/ops/test_cuda_topk_topp_sampling.py:65-91 and CUDA-test expectations :127-201; float64 brute force with explicit uniforms
+moe_route                 ops/cuda/moe/fused.py:44-100                      stable argsort + float64 softmax (ids exact, weights within one bf16 step); reference softmax-midpoint KAT tests/unit/test_cuda_moe.py:276-332
+moe_compact               ops/cuda/moe/fused.py:174-199                     reference KAT tests/ops/test_cuda_quantized_moe.py:25-67 (all sizes, modes, orders, block_m)
 merge_prefix              executor/draft_graph.py:146-157                   chain KATs tests/generation/test_tp_sampling.py:120-178
 philox_uniform            guardrail/quantized_graph/speculative.py:15-30    Random123 Philox4x32-10 known-answer vectors
 expf                      (build-fixed exp for the acceptance transform)    <= 2 ulp against libm expf over a dense sweep
@@ -298,6 +300,40 @@ def root_sample(scores, ids, temperatures, top_ps, top_ks, seeds, ordinals, *, f
     if rc:
         raise ValueError("candidate block too wide")
     return tokens, valid.astype(bool)
+
+
+def moe_route(logits_bits, activity, active_rows: int, top_k: int, *, fp16=False,
+              weights_fp16=False):
+    """Router outputs (top_logits f32, top_ids, route_ids int64, route_weights
+    uint16 bits), each [rows, top_k] (ops/cuda/moe/fused.py:44-100)."""
+    logits_bits = _c(logits_bits, np.uint16)
+    rows, experts = logits_bits.shape
+    tl_ = np.empty((rows, top_k), np.float32)
+    ti = np.empty((rows, top_k), np.int64)
+    ri = np.empty((rows, top_k), np.int64)
+    rw = np.empty((rows, top_k), np.uint16)
+    rc = lib().oracle_moe_route(_p(logits_bits), ctypes.c_int(int(fp16)), _p(_c(activity, np.int32)),
+                                ctypes.c_int(active_rows), ctypes.c_int(rows), ctypes.c_int(experts),
+                                ctypes.c_int(top_k), _p(tl_), _p(ti), _p(ri), _p(rw),
+                                ctypes.c_int(int(weights_fp16)))
+    if rc:
+        raise ValueError("invalid router geometry")
+    return tl_, ti, ri, rw
+
+
+def moe_compact(route_ids, first_expert: int, experts: int, block_m: int, row_map_fill: int = -777):
+    """(counts, starts, block_starts, total_blocks, row_map) of
+    ops/cuda/moe/fused.py:174-199; unwritten row_map slots keep ``row_map_fill``."""
+    ids = _c(route_ids, np.int64).reshape(-1)
+    counts = np.empty(experts, np.int32)
+    starts = np.empty(experts, np.int32)
+    blocks = np.empty(experts, np.int32)
+    total = np.empty(1, np.int32)
+    row_map = np.full(ids.size, row_map_fill, np.int32)
+    lib().oracle_moe_compact(_p(ids), ctypes.c_int(ids.size), ctypes.c_int(first_expert),
+                             ctypes.c_int(experts), ctypes.c_int(block_m), _p(counts), _p(starts),
+                             _p(blocks), _p(total), _p(row_map))
+    return counts, starts, blocks, int(total[0]), row_map
 
 
 def merge_prefix(decisions: np.ndarray, live_rows: int) -> np.ndarray:

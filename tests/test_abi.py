@@ -83,3 +83,14 @@ def test_root_sampler_rejects_cpu_storage():
             scores, torch.empty_like(scores, dtype=torch.int64), rows(torch.float32),
             rows(torch.float32), rows(torch.int64), rows(torch.int64), rows(torch.int64),
             rows(torch.int64), rows(torch.bool), allow_underfilled=1)
+
+
+def test_moe_router_and_compaction_arguments():
+    with pytest.raises(ValueError, match="top-k"):
+        _native.call("cubic_moe_route", 16, 0, 16, 16, 4, 16, 17, 16, 16, 16, 16, 0, None)
+    with pytest.raises(ValueError, match="experts"):
+        _native.call("cubic_moe_route", 16, 0, 16, 16, 4, 2000, 8, 16, 16, 16, 16, 0, None)
+    with pytest.raises(ValueError, match="block_m"):
+        _native.call("cubic_moe_compact", 16, 8, 0, 4, 0, 16, 16, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="experts"):
+        _native.call("cubic_moe_compact", 16, 8, 0, 1025, 16, 16, 16, 16, 16, 16, None)

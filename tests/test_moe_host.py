@@ -1,38 +1,32 @@
-"""Host logic of the routed-expert path: route compaction (no GPU)."""
+"""Host logic of the routed-expert path (no GPU): argument validation of the
+router and compaction bindings, which must fail before any launch."""
 from __future__ import annotations
 
-import numpy as np
 import pytest
 import torch
 
 from cubic_serve_amd import moe
 
 
-def brute_compaction(ids: np.ndarray, experts: int, block_m: int):
-    flat = ids.reshape(-1)
-    counts = np.array([(flat == e).sum() for e in range(experts)])
-    row_map = [r for e in range(experts) for r in range(flat.size) if flat[r] == e]
-    blocks = -(-counts // block_m)
-    return counts, np.cumsum(counts) - counts, np.cumsum(blocks) - blocks, blocks.sum(), np.array(row_map)
-
-
-@pytest.mark.parametrize("tokens,top_k,experts,block_m", [(7, 2, 4, 16), (64, 8, 32, 32), (1, 1, 3, 64)])
-def test_route_rows_matches_brute_force(tokens, top_k, experts, block_m):
-    g = torch.Generator().manual_seed(tokens * 31 + experts)
-    logits = torch.randn((tokens, experts), generator=g)
-    ids = torch.argsort(logits, dim=-1, descending=True, stable=True)[:, :top_k]
-    rows = moe.route_rows(ids, experts, block_m)
-    counts, starts, bstarts, total, row_map = brute_compaction(ids.numpy(), experts, block_m)
-    assert np.array_equal(rows.counts.numpy(), counts)
-    assert np.array_equal(rows.starts.numpy(), starts)
-    assert np.array_equal(rows.block_starts.numpy(), bstarts)
-    assert int(rows.total_blocks[0]) == total
-    assert np.array_equal(rows.row_map.numpy(), row_map)
-    assert rows.row_map.dtype == torch.int32 and rows.routing_top_k == top_k
-
-
-def test_route_rows_rejects_bad_ids():
-    with pytest.raises(ValueError):
-        moe.route_rows(torch.tensor([[0, 5]]), 4, 16)
+def test_route_rows_needs_token_by_top_k_ids():
     with pytest.raises(ValueError):
         moe.route_rows(torch.tensor([0, 1]), 4, 16)
+
+
+def test_router_binding_rejects_cpu_and_bad_abi():
+    rows, experts, k = 4, 16, 2
+    ops = (torch.zeros((rows, experts), dtype=torch.bfloat16), torch.ones(rows, dtype=torch.int32),
+           torch.tensor([rows], dtype=torch.int32), torch.empty((rows, k)),
+           torch.empty((rows, k), dtype=torch.int64), torch.empty((rows, k), dtype=torch.int64),
+           torch.empty((rows, k), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="CUDA"):
+        moe.bind_route_selection(*ops)
+    with pytest.raises(TypeError):
+        moe.bind_route_selection(*ops[:-1], None)
+
+
+def test_compaction_binding_rejects_cpu():
+    ids = torch.zeros(8, dtype=torch.int64)
+    e = lambda n: torch.empty(n, dtype=torch.int32)
+    with pytest.raises(ValueError, match="CUDA"):
+        moe.bind_compact_routes(ids, e(4), e(4), e(4), e(1), e(8), first_expert=0, experts=4, block_m=16)
