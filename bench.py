@@ -228,6 +228,8 @@ def measure_extras() -> dict:
     payload) for 64 tokens (one verify step) and 16384 tokens (prefill).
     root_sampler: top-k/top-p sampling of TP=4 x K=20 candidates for 1 and
     256 rows (T 0.8, top-p 0.9, top-k 20).
+    checkpoint: one Qwen3-8B-shaped layer loaded from safetensors and
+    repacked for the GEMM (measure_checkpoint).
     Times are per launch (HIP events, graph replays); GB/s use the
     algorithmic bytes of each launch.
     """
@@ -344,7 +346,61 @@ def measure_extras() -> dict:
         ms = time_graph(capture(lambda: [prim.launch(*ops_r) for _ in range(20)]), 10, 2) / 20
         root[f"c{rows}_us"] = round(ms * 1e3, 2)
     out["root_sampler"] = root
+    out["checkpoint"] = measure_checkpoint(dev)
     return out
+
+
+def measure_checkpoint(dev) -> dict:
+    """Load one Qwen3-8B-shaped decoder layer (qkv, o, gate, up, down; W4 g128,
+    fmt0; random payload) from a safetensors checkpoint written to a temporary
+    directory: admission, materialization on the GPU and the GEMM repack.
+    The file is in the page cache (just written), so this times the host
+    read + H2D copy + repack path, not the disk."""
+    import tempfile
+    import time
+
+    import torch
+
+    from cubic_serve_amd import checkpoint as ck, quantization as qz
+
+    g = torch.Generator().manual_seed(5)
+    shapes = {"self_attn.qkv_proj": (6144, HIDDEN), "self_attn.o_proj": (HIDDEN, HIDDEN),
+              "mlp.gate_proj": (12288, HIDDEN), "mlp.up_proj": (12288, HIDDEN),
+              "mlp.down_proj": (HIDDEN, 12288)}
+    mats = {}
+    for name, (n, k) in shapes.items():
+        groups = (n, k // GROUP)
+        mats["model.layers.0." + name] = qz.QuantizedMatrix(
+            {"weight_packed": torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.int32).to(torch.uint8),
+             "weight_scale": torch.rand(groups, generator=g) * 0.05,
+             "weight_a": (torch.rand(groups, generator=g) * 1.5 - 0.25).half(),
+             "weight_b": (torch.rand(groups, generator=g) - 0.5).half()},
+            qz.QuantizationScheme(qz.CUBIC_FORMAT, 4, GROUP), (n, k))
+    payload_bytes = sum(t.numel() * t.element_size() for m in mats.values() for t in m.payload.values())
+    with tempfile.TemporaryDirectory() as root:
+        ck.save_cubic_checkpoint(root, mats)
+        logical = [ck.LogicalWeight(name + ".weight", m.shape) for name, m in mats.items()]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plan = ck.CubicCheckpoint.admit(root, logical)
+        loaded = [plan.materialize(w, device=dev) for w in plan.weights]
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        prepared = [ck.prepare(m, dev) for m in loaded]
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        # repack kernels alone (second pass, HIP events around the launches)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        prepared = [ck.prepare(m, dev) for m in loaded]
+        end.record()
+        torch.cuda.synchronize()
+        del prepared, loaded
+    return {"layer_payload_mb": round(payload_bytes / 1e6, 1),
+            "admit_materialize_ms": round((t1 - t0) * 1e3, 1),
+            "load_gbs": round(payload_bytes / (t1 - t0) / 1e9, 2),
+            "prepare_ms": round((t2 - t1) * 1e3, 2),
+            "prepare_events_ms": round(start.elapsed_time(end), 2)}
 
 
 def main(argv=None) -> int:

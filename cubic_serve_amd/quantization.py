@@ -4,7 +4,7 @@ Mirrors the boundary types of the reference (paths under src/cubic_serve/):
   QuantizationScheme   models/quantization.py:32-56
   QuantizedMatrix      models/quantized_checkpoint.py:648-730
   payload_headers      quantization/extensions/cubic/layout.py:22-55
-  slice_index (rows)   quantization/extensions/cubic/layout.py:58-104
+  slice_index          quantization/extensions/cubic/layout.py:58-104 (rows, columns)
   parse_group          quantization/extensions/cubic/checkpoint.py:22-55
 
 The reference only decodes Cubic payloads; ``quantize_cubic`` is this build's
@@ -57,6 +57,13 @@ class QuantizationScheme:
             raise QuantizationError("activation encoding is incompatible with weight format")
 
 
+def positive_int(value: object) -> int:
+    """models/quantization.py:183-186: a group size or bit width is a positive int."""
+    if type(value) is not int or value <= 0:
+        raise QuantizationError("quantization group size must be a positive integer")
+    return value
+
+
 def parse_group(group: Mapping[str, object], weights: Mapping[str, object]) -> QuantizationScheme:
     """``cubic-pack-quantized`` config group -> scheme (checkpoint.py:22-55)."""
     if weights.get("dynamic") is not False or weights.get("symmetric") is not True:
@@ -65,10 +72,10 @@ def parse_group(group: Mapping[str, object], weights: Mapping[str, object]) -> Q
         raise QuantizationError("Cubic runtime activation transforms require a separate policy")
     size = weights.get("group_size")
     if isinstance(size, list) and len(size) == 2:
-        group_out, group_in = (int(v) for v in size)
+        group_out, group_in = (positive_int(v) for v in size)
     else:
-        group_out, group_in = 1, int(size)  # type: ignore[arg-type]
-    bits = int(weights.get("num_bits"))  # type: ignore[arg-type]
+        group_out, group_in = 1, positive_int(size)
+    bits = positive_int(weights.get("num_bits"))
     if weights.get("packing") != "little-endian-bitstream":
         raise QuantizationError("Cubic requires little-endian bitstream packing")
     if weights.get("reserved_code") != ("binary" if bits == 1 else "zero"):
@@ -146,6 +153,30 @@ class QuantizedMatrix:
             return self
         return QuantizedMatrix({k: v.to(target) for k, v in self.payload.items()}, self.encoding,
                                self.shape, self.partitions)
+
+    def columns(self, start: int, end: int) -> "QuantizedMatrix":
+        """Input-column slice (layout.py:88-104): a slice inside one original
+        group keeps that group's metadata; a multi-group slice must align to
+        groups (its end may be K); packed bytes must be whole."""
+        k = self.shape[1]
+        if not 0 <= start < end <= k:
+            raise QuantizationError("quantized slice is out of bounds")
+        e = self.encoding
+        group = e.group_in
+        one_group = start // group == (end - 1) // group
+        if not one_group and (start % group or (end % group and end != k)):
+            raise QuantizationError("input slice must preserve original scale groups")
+        if start * e.bits % 8:
+            raise QuantizationError("input slice must preserve original packed bytes")
+        payload = {}
+        for key, tensor in self.payload.items():
+            if key.endswith("_global") or key in ("weight_curve_a", "weight_curve_b"):
+                payload[key] = tensor
+            elif key == "weight_packed":
+                payload[key] = tensor[:, start * e.bits // 8:(end * e.bits + 7) // 8].contiguous()
+            else:
+                payload[key] = tensor[:, start // group:(end + group - 1) // group].contiguous()
+        return QuantizedMatrix(payload, e, (self.shape[0], end - start), self.partitions)
 
     def rows(self, start: int, end: int) -> "QuantizedMatrix":
         """Output-row slice preserving groups and partition globals (layout.py:58-86)."""
