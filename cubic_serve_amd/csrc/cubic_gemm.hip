@@ -539,19 +539,6 @@ __global__ void prepare_meta_kernel(const float* scale, const uint16_t* av, cons
     }
 }
 
-// Signed code at logical k of row `row` (reference.py:31-47 semantics).
-__device__ __forceinline__ int unpack_code(const uint8_t* rowp, int64_t row_bytes, int64_t k, int bits) {
-    const int64_t pos = k * bits, byte = pos >> 3;
-    const int shift = (int)(pos & 7);
-    uint32_t v = rowp[byte] >> shift;
-    if (shift + bits > 8) v |= (uint32_t)rowp[byte + 1 < row_bytes ? byte + 1 : row_bytes - 1] << (8 - shift);
-    const uint32_t raw = v & ((1u << bits) - 1u);
-    if (bits == 1) return (int)raw * 2 - 1;
-    const int sign = 1 << (bits - 1);
-    int q = (int)raw >= sign ? (int)raw - (1 << bits) : (int)raw;
-    return q == -sign ? 0 : q;
-}
-
 template <int BITS>
 __device__ __forceinline__ uint32_t level_sign_mask(float s, float a, float b) {
     // bit m = sign of bf16(L[m]), m = 0..7, for the stored-sign convention (bits <= 4)
@@ -567,9 +554,9 @@ __device__ __forceinline__ uint32_t level_sign_mask(float s, float a, float b) {
 }
 
 template <int BITS>
-__global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, const uint16_t* av,
-                                     const uint16_t* bv, int64_t n, int64_t k, int group_in,
-                                     int groups_k, int n_tiles, int k_blocks, uint32_t* codes) {
+__global__ __launch_bounds__(kThreads) void prepare_codes_kernel(
+        const uint8_t* packed, const float* scale, const uint16_t* av, const uint16_t* bv, int64_t n,
+        int64_t k, int group_in, int groups_k, int n_tiles, int k_blocks, int aligned, uint32_t* codes) {
     const int64_t total = (int64_t)n_tiles * k_blocks * kWave;
     const int64_t row_bytes = (k * BITS + 7) / 8;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -579,7 +566,6 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
         const int q = lane >> 4, col = lane & 15;
         const int64_t row = nt * 16 + col;
         const int64_t k0 = kb * kKBlock + 32 * q;
-        int mag[32], neg[32];
         float s = 0.0f, a = 0.0f, b = 0.0f;
         if (row < n && k0 < k) {
             const int64_t g = k0 / group_in;
@@ -588,9 +574,38 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
             b = half_bits_to_float(bv[row * groups_k + g]);
         }
         const uint32_t sigma = BITS <= 4 ? level_sign_mask<BITS>(s, a, b) : 0u;
+        // codes k0 .. k0+31 of the row: 4 * BITS bytes of the little-endian
+        // bitstream starting at byte k0 * BITS / 8 (a multiple of 4)
+        uint32_t rw[BITS + 1];
+#pragma unroll
+        for (int x = 0; x <= BITS; ++x) rw[x] = 0;
+        if (row < n && k0 < k) {
+            const uint8_t* src = packed + row * row_bytes + k0 * BITS / 8;
+            if (aligned && k0 + 32 <= k) {
+#pragma unroll
+                for (int x = 0; x < BITS; ++x) rw[x] = reinterpret_cast<const uint32_t*>(src)[x];
+            } else {
+                const int64_t left = row_bytes - k0 * BITS / 8;
+#pragma unroll
+                for (int y = 0; y < 4 * BITS; ++y)
+                    if (y < left) rw[y >> 2] |= (uint32_t)src[y] << (8 * (y & 3));
+            }
+        }
+        int mag[32], neg[32];
+#pragma unroll
         for (int e = 0; e < 32; ++e) {
-            int qv = 0;
-            if (row < n && k0 + e < k) qv = unpack_code(packed + row * row_bytes, row_bytes, k0 + e, BITS);
+            const int p = BITS * e, word = p >> 5, shift = p & 31;
+            const uint64_t pair = ((uint64_t)rw[word + 1] << 32) | rw[word];
+            const int raw = (int)((pair >> shift) & ((1u << BITS) - 1u));
+            int qv;
+            if constexpr (BITS == 1) {
+                qv = raw * 2 - 1;
+            } else {
+                constexpr int kSign = 1 << (BITS - 1);
+                qv = raw >= kSign ? raw - (1 << BITS) : raw;
+                if (qv == -kSign) qv = 0;  // reserved code
+            }
+            if (row >= n || k0 + e >= k) qv = 0;
             const int m = qv < 0 ? -qv : qv;
             mag[e] = m;
             if (BITS <= 4)  // stored sign = sign(q) xor sign(bf16(L[|q|]))
@@ -600,7 +615,9 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
         }
         uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (BITS == 4) {
+#pragma unroll
             for (int f = 0; f < 4; ++f)
+#pragma unroll
                 for (int byte = 0; byte < 4; ++byte) {
                     const int ea = 8 * f + byte, eb = 8 * f + 4 + byte;
                     const uint32_t v = (uint32_t)(mag[ea] & 7) | ((uint32_t)neg[eb] << 3) |
@@ -608,7 +625,9 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
                     w[f] |= v << (8 * byte);
                 }
         } else if (BITS == 3 || BITS == 2 || BITS == 1) {
+#pragma unroll
             for (int f = 0; f < 4; ++f)
+#pragma unroll
                 for (int byte = 0; byte < 4; ++byte) {
                     const int ea = 8 * f + byte, eb = 8 * f + 4 + byte;
                     if (BITS == 3) {
@@ -623,6 +642,7 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
                              ((uint32_t)neg[eb] << (8 * byte + 6 - 2 * f));
                 }
         } else {
+#pragma unroll
             for (int e = 0; e < 32; ++e) {
                 const uint32_t code = ((uint32_t)neg[e] << (BITS - 1)) | (uint32_t)mag[e];
                 const int p = BITS * e, word = p >> 5, shift = p & 31;
@@ -630,6 +650,7 @@ __global__ void prepare_codes_kernel(const uint8_t* packed, const float* scale, 
                 if (shift + BITS > 32) w[word + 1] |= code >> (32 - shift);
             }
         }
+#pragma unroll
         for (int x = 0; x < BITS; ++x) codes[i * BITS + x] = w[x];
     }
 }
@@ -735,8 +756,9 @@ hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t
     const int64_t code_threads = (int64_t)n_tiles * k_blocks * kWave;
     const int blocks = (int)((code_threads + 255) / 256 < 65535 ? (code_threads + 255) / 256 : 65535);
     const uint8_t* p = (const uint8_t*)packed;
+    const int aligned = ((uintptr_t)packed % 4 == 0) && (((k * bits + 7) / 8) % 4 == 0);
     switch (bits) {
-#define CUBIC_PREP(B) case B: prepare_codes_kernel<B><<<blocks, 256, 0, s>>>(p, scale, av, bv, n, k, group_in, groups_k, n_tiles, k_blocks, codes); break;
+#define CUBIC_PREP(B) case B: prepare_codes_kernel<B><<<blocks, 256, 0, s>>>(p, scale, av, bv, n, k, group_in, groups_k, n_tiles, k_blocks, aligned, codes); break;
         CUBIC_PREP(1) CUBIC_PREP(2) CUBIC_PREP(3) CUBIC_PREP(4)
         CUBIC_PREP(5) CUBIC_PREP(6) CUBIC_PREP(7) CUBIC_PREP(8)
 #undef CUBIC_PREP
