@@ -15,8 +15,9 @@
 // every depth and merges the prefix.  Arrival counters live in the caller's
 // workspace; the finishing workgroup returns its counter to zero.
 //
-// Wave-level reductions follow fixed orders (butterfly sums, Kogge-Stone
-// scans) that the CPU restatement reproduces operation for operation.
+// Wave-level reductions follow fixed orders (butterfly sums in ascending
+// lane distance, row-wise scans; cubic_device.h) that the CPU restatement
+// reproduces operation for operation.
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
 
@@ -214,45 +215,31 @@ struct LaneSet {
 
 template <int SLOTS>
 __device__ __forceinline__ float vl_tree_sum(float (&x)[SLOTS], int block) {
-    // butterfly x[i] += x[i ^ m], m = block/2 .. 1
-    for (int m = block >> 1; m >= 1; m >>= 1) {
-        if (m >= kWave) {
-            const int sm = m / kWave;
-            float y[SLOTS];
+    // butterfly x[i] += x[i ^ m], m = 1, 2, ..., block/2: lanes, then slots
+    const int width = block < kWave ? block : kWave;
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) y[s] = x[s] + x[s ^ sm];
+    for (int s = 0; s < SLOTS; ++s) x[s] = wave_butterfly_sum(x[s], width);
+    for (int m = kWave; m < block; m <<= 1) {
+        const int sm = m / kWave;
+        float y[SLOTS];
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
-        } else {
+        for (int s = 0; s < SLOTS; ++s) y[s] = x[s] + x[s ^ sm];
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) x[s] = x[s] + __shfl_xor(x[s], m);
-        }
+        for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
     }
     return __shfl(x[0], 0);
 }
 
 template <int SLOTS>
 __device__ __forceinline__ void vl_scan(float (&x)[SLOTS], int block, int lane) {
-    // Kogge-Stone inclusive scan x[i] += x[i - d], d = 1 .. block/2
-    for (int d = 1; d < block; d <<= 1) {
-        float y[SLOTS];
-        if (d >= kWave) {
-            const int sd = d / kWave;
+    // inclusive scan: row-wise order of wave_row_scan inside each slot, then
+    // each slot adds the previous slot's last lane, slot after slot
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) y[s] = s >= sd ? x[s] + x[s - sd] : x[s];
-        } else {
+    for (int s = 0; s < SLOTS; ++s) x[s] = wave_row_scan(x[s]);
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) {
-                const float same = __shfl(x[s], lane - d);                          // lane >= d
-                const float prev = __shfl(x[s > 0 ? s - 1 : 0], lane + kWave - d);  // lane < d
-                const int v = lane + kWave * s;
-                const float other = lane >= d ? same : prev;
-                y[s] = v >= d ? x[s] + other : x[s];
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
-    }
+    for (int s = 1; s < SLOTS; ++s)
+        if (kWave * s < block) x[s] = x[s] + __shfl(x[s - 1], kWave - 1);
+    (void)lane;
 }
 
 template <int SLOTS>
@@ -260,11 +247,8 @@ __device__ __forceinline__ float vl_max(const float (&x)[SLOTS], int block) {
     float m = -__builtin_huge_valf();
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) m = x[s] > m ? x[s] : m;  // NaN-ignoring
-    for (int w = (block < kWave ? block : kWave) >> 1; w >= 1; w >>= 1) {
-        const float o = __shfl_xor(m, w);
-        m = o > m ? o : m;
-    }
-    return __shfl(m, 0);
+    (void)block;  // lanes past the block hold -inf
+    return __shfl(wave_max_f32(m), 0);
 }
 
 __device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
@@ -556,21 +540,28 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
 // --------------------------------------------------------------------------
 constexpr int kRootThreads = 256;
 
-struct RootEntry {
-    float score;
-    uint32_t flags;  // bit 0 real, bit 1 first
-    int64_t id;
-};
-
 struct RootScratch {
-    RootEntry e[kRootThreads];
+    uint64_t key[kRootThreads];      // (sortable score << 32) | ~id32 of real lanes, else 0
+    float score[kRootThreads];
+    int64_t id[kRootThreads];
+    uint32_t real[kRootThreads];
+    float sorted_score[kRootThreads];  // real pairs at their (score desc, id asc, lane asc) rank
+    int64_t sorted_id[kRootThreads];
+    int counts[kRootThreads / kWave][4];
     float sel_score[kWave];
     int64_t sel_id[kWave];
 };
 
+// Monotone map of a finite float to uint32 (-0 and +0 map alike).
+__device__ __forceinline__ uint32_t sortable_score(float f) {
+    const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArgs a) {
     __shared__ RootScratch sc;
-    const int row = blockIdx.x, v = threadIdx.x;
+    const int row = blockIdx.x, v = threadIdx.x, w = v / kWave, lane = v % kWave;
+    ACC_STAMP(0);
     const int count = a.tp * a.k;
     const bool cm = v < count;
     float score = -__builtin_huge_valf();
@@ -583,36 +574,70 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     }
     const bool real = cm && id >= 0 && __builtin_fabsf(score) < __builtin_huge_valf();
     const bool sentinel = cm && score != score && id == -1;
-    sc.e[v].score = score;
-    sc.e[v].id = id;
-    sc.e[v].flags = real ? 1u : 0u;
+    const bool wide = real && (uint64_t)id > 0xFFFFFFFFull;
+    const uint64_t key = real ? ((uint64_t)sortable_score(score) << 32) | (0xFFFFFFFFu - (uint32_t)id) : 0ull;
+    sc.key[v] = key;
+    sc.score[v] = score;
+    sc.id[v] = id;
+    sc.real[v] = real;
     if (v < kWave) { sc.sel_score[v] = -__builtin_huge_valf(); sc.sel_id[v] = kInt64Max; }
-    const int malformed = __syncthreads_count(cm && !real && !sentinel);
-    const int real_count = __syncthreads_count(real);
-    // Branch-free passes over uniform (broadcast) LDS entries, unrolled so
-    // the reads of several entries are in flight together.
-    uint32_t dup = 0;
-#pragma unroll 8
-    for (int j = 0; j < count; ++j) {
-        const RootEntry o = sc.e[j];
-        dup |= (uint32_t)(j < v) & o.flags & (uint32_t)(o.score == score) & (uint32_t)(o.id == id);
+    {
+        const uint64_t bm = __ballot(cm && !real && !sentinel), br = __ballot(real), bw = __ballot(wide);
+        if (lane == 0) {
+            sc.counts[w][0] = __builtin_popcountll(bm);
+            sc.counts[w][1] = __builtin_popcountll(br);
+            sc.counts[w][2] = __builtin_popcountll(bw);
+        }
     }
-    const bool first = real && !dup;
+    ACC_STAMP(1);
     __syncthreads();
-    if (first) sc.e[v].flags = 3u;
-    __syncthreads();
+    int malformed = 0, real_count = 0, wide_count = 0;
+#pragma unroll
+    for (int x = 0; x < kRootThreads / kWave; ++x) {
+        malformed += sc.counts[x][0];
+        real_count += sc.counts[x][1];
+        wide_count += sc.counts[x][2];
+    }
+    // rank of a real pair in (score desc, id asc, lane asc): unique 0 .. real_count-1.
+    // One pass over broadcast LDS entries; 64-bit keys unless an id needs more
+    // than 32 bits.
     int rank = 0;
+    if (wide_count == 0) {
 #pragma unroll 8
-    for (int j = 0; j < count; ++j) {
-        const RootEntry o = sc.e[j];
-        const uint32_t ahead = (uint32_t)(o.score > score) | ((uint32_t)(o.score == score) & (uint32_t)(o.id < id));
-        rank += (int)((o.flags >> 1) & ahead);
+        for (int j = 0; j < count; ++j) {
+            const uint64_t o = sc.key[j];
+            rank += (int)((uint32_t)(o > key) | ((uint32_t)(o == key) & (uint32_t)(j < v)));
+        }
+    } else {
+#pragma unroll 4
+        for (int j = 0; j < count; ++j) {
+            const float os = sc.score[j];
+            const int64_t oi = sc.id[j];
+            const uint32_t ahead = (uint32_t)(os > score) |
+                                   ((uint32_t)(os == score) & ((uint32_t)(oi < id) | ((uint32_t)(oi == id) & (uint32_t)(j < v))));
+            rank += (int)(sc.real[j] & ahead);
+        }
     }
-    if (first && rank < a.k) { sc.sel_score[rank] = score; sc.sel_id[rank] = id; }
+    ACC_STAMP(2);
+    if (real) { sc.sorted_score[rank] = score; sc.sorted_id[rank] = id; }
+    __syncthreads();
+    // a sorted pair equal to its predecessor is a duplicate: it takes no slot
+    // (the reference removes every copy of the pair it selects)
+    const bool in = v < real_count;
+    const float ps = in ? sc.sorted_score[v] : 0.0f;
+    const int64_t pi = in ? sc.sorted_id[v] : 0;
+    const bool dup = in && v > 0 && sc.sorted_score[v - 1] == ps && sc.sorted_id[v - 1] == pi;
+    const uint64_t bd = __ballot(dup);
+    if (lane == 0) sc.counts[w][3] = __builtin_popcountll(bd);
+    __syncthreads();
+    int dups_before = __builtin_popcountll(bd & (lane ? (~0ull >> (kWave - lane)) : 0ull));
+    for (int x = 0; x < w; ++x) dups_before += sc.counts[x][3];
+    const int distinct = v - dups_before;
+    if (in && !dup && distinct < a.k) { sc.sel_score[distinct] = ps; sc.sel_id[distinct] = pi; }
     __syncthreads();
     if (v >= kWave) return;
+    ACC_STAMP(3);
 
-    const int lane = v;
     const float temperature = a.temperatures[row], top_p = a.top_ps[row];
     const int64_t top_k = a.top_ks[row], seed = a.seeds[row], ordinal = a.ordinals[row];
     const bool greedy = temperature == 0.0f;
@@ -627,10 +652,12 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     const int64_t sel_id = sc.sel_id[lane];
     float retained[1], mass;
     probabilities<1, false>(sorted, temperature, top_k, top_p, kWave, lane, retained, mass);
+    ACC_STAMP(4);
     const int64_t random_seed = seed ^ (seed >> 32) ^ (ordinal >> 32);
     const float uniform = philox_uniform2((uint32_t)random_seed, (uint32_t)((uint64_t)random_seed >> 32),
                                           (uint32_t)ordinal);
     const float target = uniform * mass;
+    ACC_STAMP(5);
     vl_scan<1>(retained, kWave, lane);
     const uint64_t hit = __ballot(retained[0] > target);
     const int sampled = hit ? __builtin_ctzll(hit) : kWave;
@@ -638,6 +665,7 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     const int64_t token = __shfl(sel_id, chosen & (kWave - 1));
     const bool valid = malformed == 0 && params_ok && enough &&
                        (greedy || (mass > 0.0f && sampled < kWave));
+    ACC_STAMP(6);
     if (lane == 0) {
         a.output_tokens[row] = valid ? token : -1;
         a.output_valid[row] = valid ? 1 : 0;

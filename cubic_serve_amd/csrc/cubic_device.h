@@ -138,6 +138,58 @@ __device__ __forceinline__ float philox_uniform(uint32_t key, uint32_t ordinal) 
     return philox_uniform2(key, 0u, ordinal);
 }
 
+// ---------------------------------------------------------------------------
+// Wave reductions in fixed orders (the CPU restatement follows the same
+// orders).  DPP exchanges (gfx9 encodings): quad_perm [1,0,3,2] 0xB1,
+// [2,3,0,1] 0x4E, row_half_mirror 0x141, row_mirror 0x140, row_shr:d 0x110+d,
+// row_bcast:15 0x142, row_bcast:31 0x143.  A lane whose source is invalid,
+// or whose row is masked off, reads 0.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_or_zero(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Butterfly sum x[i] += x[i ^ m] for m = 1, 2, 4, ... < width (width a power of
+// two <= 64): every lane of an aligned width-group ends with the group total.
+// m = 4 and m = 8 read the half-row / row mirror: after the steps below m
+// every lane of a quad (of an 8-group) holds the same value, so the mirror
+// lane's value is the xor partner's.
+__device__ __forceinline__ float wave_butterfly_sum(float x, int width) {
+    if (width > 1) x = x + dpp_or_zero<0xB1>(x);
+    if (width > 2) x = x + dpp_or_zero<0x4E>(x);
+    if (width > 4) x = x + dpp_or_zero<0x141>(x);
+    if (width > 8) x = x + dpp_or_zero<0x140>(x);
+    if (width > 16) x = x + __shfl_xor(x, 16);
+    if (width > 32) x = x + __shfl_xor(x, 32);
+    return x;
+}
+
+// Maximum over the 64 lanes (exact in any order; NaN-ignoring).
+__device__ __forceinline__ float wave_max_f32(float x) {
+    float o;
+    o = dpp_or_zero<0xB1>(x); x = o > x ? o : x;
+    o = dpp_or_zero<0x4E>(x); x = o > x ? o : x;
+    o = dpp_or_zero<0x141>(x); x = o > x ? o : x;
+    o = dpp_or_zero<0x140>(x); x = o > x ? o : x;
+    o = __shfl_xor(x, 16); x = o > x ? o : x;
+    o = __shfl_xor(x, 32); x = o > x ? o : x;
+    return x;
+}
+
+// Inclusive scan over the 64 lanes: inside each 16-lane row x[i] += x[i - d]
+// for d = 1, 2, 4, 8 (i % 16 >= d); then rows 1 and 3 add lane 15 and lane 47;
+// then rows 2 and 3 add lane 31.
+__device__ __forceinline__ float wave_row_scan(float x) {
+    x = x + dpp_or_zero<0x111>(x);
+    x = x + dpp_or_zero<0x112>(x);
+    x = x + dpp_or_zero<0x114>(x);
+    x = x + dpp_or_zero<0x118>(x);
+    x = x + dpp_or_zero<0x142, 0xA>(x);
+    x = x + dpp_or_zero<0x143, 0xC>(x);
+    return x;
+}
+
 // Cross-workgroup hand-off without a full cache write-back: the producer
 // writes the exchanged words with device-scope atomic stores, drains its
 // memory counters, then bumps an arrival counter; the last arrival reads the

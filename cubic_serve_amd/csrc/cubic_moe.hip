@@ -9,7 +9,7 @@
 //
 // Router, per row: the top_k experts by (logit desc, expert id asc); their
 // logits and ids in that order; softmax over the selected logits (max
-// subtracted, build-defined exp, butterfly sum) and the (id, weight) pairs
+// subtracted, build-defined exp, ascending butterfly sum) and the (id, weight) pairs
 // re-ordered by ascending expert id.  Rows at or past *active_rows, or with
 // row_activity 0, publish logits 0, ids -1, route ids -1 and weights 0.
 //
@@ -77,16 +77,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoERouteArgs a
         a.top_ids[(int64_t)row * k + lane] = active ? id : -1;
     }
     // softmax over the selected logits: max, exp(s - max), butterfly sum
-    float mx = score;
-#pragma unroll
-    for (int w = kWave / 2; w >= 1; w >>= 1) {
-        const float o = __shfl_xor(mx, w);
-        mx = o > mx ? o : mx;
-    }
+    const float mx = wave_max_f32(score);
     const float p = slot ? accept_expf(score - mx) : 0.0f;
-    float sum = p;
-#pragma unroll
-    for (int m = kWave / 2; m >= 1; m >>= 1) sum = sum + __shfl_xor(sum, m);
+    const float sum = wave_butterfly_sum(p, kWave);
     // output slot = number of selected ids below this one
     int out = 0;
     for (int j = 0; j < k; ++j) out += __shfl(id, j) < id ? 1 : 0;

@@ -368,14 +368,17 @@ static void select_topk(float* scores, int64_t* ids, const int* real, int lanes,
 }
 
 /* Reduction orders.  Triton leaves tl.sum / tl.cumsum order open; this
- * build fixes them to what a 64-lane wavefront does with lane shuffles:
- *   tree_sum: butterfly, x[i] += x[i ^ m] for m = BLOCK/2 .. 1 (every lane
- *             ends with the same total because binary32 + commutes);
- *   ks_scan:  Kogge-Stone inclusive scan, x[i] += x[i - d] for d = 1 .. BLOCK/2. */
+ * build fixes them to what a 64-lane wavefront does with DPP lane exchanges:
+ *   tree_sum: butterfly, x[i] += x[i ^ m] for m = 1, 2, 4, .. BLOCK/2 (every
+ *             lane ends with the same total because binary32 + commutes);
+ *   row_scan: inclusive scan in 64-lane groups: inside each 16-lane row
+ *             x[i] += x[i - d] for d = 1, 2, 4, 8 (i % 16 >= d); rows 1 and 3
+ *             add lane 15 / lane 47; rows 2 and 3 add lane 31; then each
+ *             64-lane group adds the last lane of the group before it. */
 static float tree_sum(const float* in, int lanes) {
     float x[MAX_LANES], y[MAX_LANES];
     for (int l = 0; l < lanes; ++l) x[l] = in[l];
-    for (int m = lanes / 2; m >= 1; m >>= 1) {
+    for (int m = 1; m < lanes; m <<= 1) {
         for (int l = 0; l < lanes; ++l) y[l] = x[l] + x[l ^ m];
         for (int l = 0; l < lanes; ++l) x[l] = y[l];
     }
@@ -385,10 +388,23 @@ static float tree_sum(const float* in, int lanes) {
 static void ks_scan(const float* in, int lanes, float* out) {
     float x[MAX_LANES], y[MAX_LANES];
     for (int l = 0; l < lanes; ++l) x[l] = in[l];
-    for (int d = 1; d < lanes; d <<= 1) {
-        for (int l = 0; l < lanes; ++l) y[l] = l >= d ? x[l] + x[l - d] : x[l];
-        for (int l = 0; l < lanes; ++l) x[l] = y[l];
+    for (int g = 0; g < lanes; g += 64) {
+        const int n = lanes - g < 64 ? lanes - g : 64;
+        float* z = x + g;
+        for (int d = 1; d <= 8; d <<= 1) {
+            for (int l = 0; l < n; ++l) y[l] = (l % 16 >= d) ? z[l] + z[l - d] : z[l];
+            for (int l = 0; l < n; ++l) z[l] = y[l];
+        }
+        for (int l = 0; l < n; ++l) {
+            const int r = l / 16;
+            y[l] = (r == 1) ? z[l] + z[15] : (r == 3) ? z[l] + z[47] : z[l];
+        }
+        for (int l = 0; l < n; ++l) z[l] = y[l];
+        for (int l = 0; l < n; ++l) y[l] = (l / 16 >= 2) ? z[l] + z[31] : z[l];
+        for (int l = 0; l < n; ++l) z[l] = y[l];
     }
+    for (int g = 64; g < lanes; g += 64)
+        for (int l = 0; l < 64 && g + l < lanes; ++l) x[g + l] = x[g + l] + x[g - 1];
     for (int l = 0; l < lanes; ++l) out[l] = x[l];
 }
 
