@@ -92,15 +92,20 @@ __global__ __launch_bounds__(kEmbedThreads) void embedding_kernel(EmbedArgs a) {
     constexpr int kSlice = kEmbedThreads * kEmbedCols;
     __shared__ float t_table[kMags];
     __shared__ uint16_t lut[LUT ? kSlice / 4 : 1];
+    const int64_t token = blockIdx.x;
+    const int64_t row = a.id_bytes == 8 ? ((const int64_t*)a.ids)[token]
+                                        : (int64_t)((const int32_t*)a.ids)[token];
+    const bool live = row >= 0 && row < a.n;  // uniform over the workgroup
+    const int64_t c = (int64_t)blockIdx.y * kEmbedThreads + threadIdx.x;
+    const int64_t col0 = c * kEmbedCols;
+    // the row's codes are requested first: their latency overlaps the tables
+    uint32_t w[5] = {0, 0, 0, 0, 0};
+    if (live && col0 < a.k) load_chunk<BITS>(a.packed + row * a.row_bytes, c, a.row_bytes, a.aligned, w);
     if (BITS > 1) {
         for (int m = threadIdx.x; m < kMags; m += kEmbedThreads)
             t_table[m] = (float)((double)m / (double)(kMags - 1));
         __syncthreads();
     }
-    const int64_t token = blockIdx.x;
-    const int64_t row = a.id_bytes == 8 ? ((const int64_t*)a.ids)[token]
-                                        : (int64_t)((const int32_t*)a.ids)[token];
-    const bool live = row >= 0 && row < a.n;  // uniform over the workgroup
     const int p = live && a.fmt != 0 ? a.part_of_row[row] : 0;
     const int64_t meta_row = (row / a.group_out) * a.groups_k;
     const int64_t slice0 = (int64_t)blockIdx.y * kSlice;
@@ -121,16 +126,12 @@ __global__ __launch_bounds__(kEmbedThreads) void embedding_kernel(EmbedArgs a) {
         }
         __syncthreads();
     }
-    const int64_t c = (int64_t)blockIdx.y * kEmbedThreads + threadIdx.x;
-    const int64_t col0 = c * kEmbedCols;
     if (col0 >= a.k) return;
     const int cnt = a.k - col0 < kEmbedCols ? (int)(a.k - col0) : kEmbedCols;
     uint32_t h[kEmbedCols / 2];
 #pragma unroll
     for (int i = 0; i < kEmbedCols / 2; ++i) h[i] = 0;
     if (live) {
-        uint32_t w[5];
-        load_chunk<BITS>(a.packed + row * a.row_bytes, c, a.row_bytes, a.aligned, w);
         if constexpr (LUT) {
             const uint16_t* tab = lut + (((col0 - slice0) / a.group_in) << BITS);
 #pragma unroll
