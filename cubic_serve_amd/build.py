@@ -3,6 +3,7 @@
 hipcc cross-compiles on a machine without a GPU.  Flags:
   -ffp-contract=off   the Cubic decoder and acceptance transform are unfused IEEE
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed FP32 instructions
+  -mllvm -amdgpu-mfma-vgpr-form   MFMA accumulators in VGPRs (no AGPR copies)
 """
 from __future__ import annotations
 
@@ -32,6 +33,7 @@ def flags() -> list[str]:
     return [
         f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
         f"-I{ROOT / 'include'}", f"-I{CSRC}",
     ]

@@ -199,10 +199,12 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&dst)[
     }
 }
 
-// Prefetch depth (k-blocks of codes in flight per wave) by code words per tile.
+// Code/metadata prefetch depth in k-blocks.  Two: deeper rings cost the
+// registers of a third resident workgroup per CU and measured slower on every
+// cfg2 shape.
 template <int BITS, int J>
-struct Stages {  // a power of two: divides the usual per-split k-block counts
-    static constexpr int value = (J * BITS <= 4) ? 8 : (J * BITS <= 16 ? 4 : 2);
+struct Stages {
+    static constexpr int value = 2;
 };
 
 // Last arrival of a split-K output block: sums the S partitions of each unit
@@ -243,8 +245,12 @@ __device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buff
     }
 }
 
-template <int BITS, int MT, int J, bool G128>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
+// OCC3: registers capped for three resident workgroups per CU (the wide
+// single-split launches: lm_head-sized N with J = 2, MT = 4; the cap only
+// spills in the split-K exchange, which those launches do not run).
+template <int BITS, int MT, int J, bool G128, bool OCC3 = false>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(OCC3 ? 3 : 1)))
+void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
     constexpr int S = Stages<BITS, J>::value;
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
@@ -327,7 +333,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     // With MT = 1 threads also load rows 16..31 (never read by the MFMAs).
     // Two register stages: the block for kb + 2 is in flight while kb is used.
     constexpr int kAct = (16 * MT * 16 + kGemmThreads - 1) / kGemmThreads;
-    uint4 act[2][kAct];
+    // One register stage: the block for kb + 1 is in flight while kb is
+    // staged (a second stage measured no faster and costs 16 registers).
+    constexpr int NA = 1;
+    uint4 act[NA][kAct];
     const uint16_t* act_row[kAct];
     int act_r[kAct];
     const int act_c8 = (threadIdx.x & 15) * 8;  // same chunk column for every i
@@ -349,8 +358,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     CUBIC_STAMP(0);
 #pragma unroll
     for (int st = 0; st < S; ++st) load_codes(kb_begin + st, ring_codes[st], ring_meta[st]);
-    load_act(kb_begin, act[0]);
-    load_act(kb_begin + 1, act[1]);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) load_act(kb_begin + i, act[i]);
     // Whole groups of S k-blocks, with no exit inside the unrolled group (an
     // exit there makes the wait-count analysis drain the ring at the loop
     // edge).  Blocks past the split's end read clamped addresses and get zero
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < kAct; ++i) {
                 const int r = act_r[i];
-                const uint4 v = act[ab][i];
+                const uint4 v = act[st % NA][i];
                 *reinterpret_cast<uint4*>(&lds[((r >> 4) * 256 + a_slot(r & 15, act_c8 >> 3)) * 8]) =
                     make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
             }
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
             CUBIC_STAMP(1 + kb - kb_begin);
-            load_act(kb + 2, act[ab]);
+            load_act(kb + NA, act[st % NA]);
             __builtin_amdgcn_sched_barrier(0);  // keep the prefetch where it is issued
 
             // level tables (bits <= 4, prepared) or curve parameters (bits >= 5)
@@ -412,8 +421,6 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
             };
             // A fragments are double-buffered: the LDS reads of fragment f + 1
             // are in flight while fragment f is decoded and multiplied.
-            // A fragments are double-buffered: the LDS reads of fragment f + 1
-            // are in flight while fragment f is decoded and multiplied.
             bf16x8_t afrag_buf[2][MT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) afrag_buf[0][mt] = afrag_at(mt, 0);
@@ -423,6 +430,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) afrag_buf[(f + 1) & 1][mt] = afrag_at(mt, f + 1);
                 }
+                const int fb = f & 1;
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     uint4 bw;
@@ -433,7 +441,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
                     const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag_buf[f & 1][mt], bfrag,
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag_buf[fb][mt], bfrag,
                                                                              acc[mt][j], 0, 0, 0);
                 }
             }
@@ -677,6 +685,12 @@ hipError_t launch_g(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
 #ifdef CUBIC_TIMELINE
     if (j == 4) { gemm_kernel<BITS, MT, 4, G128><<<grid, kGemmThreads, 0, s>>>(a); return hipGetLastError(); }
 #endif
+    if constexpr (MT == 4 && BITS <= 5) {
+        if (j == 2 && a.split == 1) {
+            gemm_kernel<BITS, MT, 2, G128, true><<<grid, kGemmThreads, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    }
     if (j == 2) gemm_kernel<BITS, MT, 2, G128><<<grid, kGemmThreads, 0, s>>>(a);
     else gemm_kernel<BITS, MT, 1, G128><<<grid, kGemmThreads, 0, s>>>(a);
     return hipGetLastError();
