@@ -50,25 +50,29 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
     GemmPlan p;
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
-    p.tiles_per_wave = 1;
-    // Two 16-column tiles per wave once that still leaves >= 128 column
-    // blocks (halves the activation bytes and A-fragment LDS reads per weight
-    // byte); four would drop to one wave per SIMD (register bound).
-    if (ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) >= 128) p.tiles_per_wave = 2;
+    const int64_t chunks = ceil_div(m, 64);
+    int split = 1;
+    if (ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) * chunks >= 256) {
+        // Wide outputs (lm_head): two 16-column tiles per wave (half the
+        // activation bytes and A-fragment LDS reads per weight byte) and
+        // enough column blocks to fill the GPU without a K split, which also
+        // admits the three-workgroups-per-CU register cap.
+        p.tiles_per_wave = 2;
+    } else {
+        // Narrower outputs: one tile per wave, K split until a partition has
+        // at most 16 k-blocks and about 256 workgroups are in flight (measured
+        // best on the cfg2 layer shapes: qkv / o split 4, down split 8, gate/up
+        // split 2).
+        p.tiles_per_wave = 1;
+        const int64_t out_blocks = ceil_div(p.n_tiles, cubic::kGemmWaves) * chunks;
+        while (split < 8 && (ceil_div(p.k_blocks, split) > 16 || out_blocks * split < 256)) split *= 2;
+        if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
+    }
 #ifdef CUBIC_TIMELINE  // instrumented build only: plan overrides for sweeps
     if (const char* e = getenv("CUBIC_DEV_J")) p.tiles_per_wave = atoi(e);
-#endif
-    p.col_blocks = (int)ceil_div(p.n_tiles, cubic::kGemmWaves * p.tiles_per_wave);
-    // K is split until about 256 workgroups are in flight (one per CU): more
-    // partitions cost more in the exchange than they gain in parallelism.
-    const int64_t out_blocks = (int64_t)p.col_blocks * ceil_div(m, 64);
-    int split = 1;
-    while (split < 8 && out_blocks * split < 256) split *= 2;
-    if (split > 8) split = 8;
-    if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
-#ifdef CUBIC_TIMELINE
     if (const char* e = getenv("CUBIC_DEV_SPLIT")) split = atoi(e);
 #endif
+    p.col_blocks = (int)ceil_div(p.n_tiles, cubic::kGemmWaves * p.tiles_per_wave);
     p.blocks_per_split = (int)ceil_div(p.k_blocks, split);
     p.split = (int)ceil_div(p.k_blocks, p.blocks_per_split);
     return p;
@@ -390,9 +394,9 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
     cubic_prepared_words(n, k, bits, group_in, &cw, &mw);
     if (expert_code_words < cw || expert_meta_words < mw)
         return fail(CUBIC_EINVAL, "expert strides smaller than one prepared matrix");
-    // one 64-row chunk plan: J and no K split (routed launches have
-    // max_blocks x column blocks workgroups)
-    const GemmPlan p = plan_gemm(64 * 256, n, k);
+    // no K split (routed launches have max_blocks x column blocks
+    // workgroups); two tiles per wave once there are >= 128 column blocks
+    const GemmPlan p = plan_gemm(64, n, k);
     cubic::GemmArgs a = {};
     a.x = (const uint16_t*)x;
     a.codes = codes;
@@ -411,7 +415,7 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
     a.split = 1;
     a.blocks_per_split = p.k_blocks;
     a.n_tiles = p.n_tiles;
-    a.tiles_per_wave = p.tiles_per_wave;
+    a.tiles_per_wave = ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) >= 128 ? 2 : 1;
     a.routed = 1;
     a.block_m = block_m;
     a.padded = padded;
