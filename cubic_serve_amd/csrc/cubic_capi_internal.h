@@ -9,7 +9,8 @@ namespace cubic {
 // GEMM workgroup: kGemmWaves waves, each owning J 16-column tiles, share one
 // LDS activation tile.  Four: two independent workgroups per CU hide latency
 // better than one 8-wave workgroup in barrier lockstep, although the latter
-// halves the activation bytes per weight byte (measured both).
+// halves the activation bytes per weight byte (measured both); 2-wave
+// workgroups measured slower on every cfg2 shape.
 constexpr int kGemmWaves = 4;
 
 struct AcceptArgs {
