@@ -494,7 +494,7 @@ def main(argv=None) -> int:
         "layers_us": round((ms_per_step - lm_ms - acc_ms) * 1e3, 2),
         "greedy_accepted": f"{accepted}/{C_SEQ}",
         "wall_s": round(wall, 3),
-        "roofline": {"kernel": "gemm_kernel<4,4,2,true> (lm_head)", "bound": "hbm",
+        "roofline": {"kernel": "gemm_kernel<4,4,2,true,true> (lm_head)", "bound": "hbm",
                      "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": nb["lm_head"]},
