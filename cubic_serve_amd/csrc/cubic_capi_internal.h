@@ -119,6 +119,7 @@ struct GemmArgs {
     int split, blocks_per_split;  // K partitions and k-blocks per partition
     int n_tiles;                  // ceil(n / 16)
     int tiles_per_wave;           // J: 16-column tiles per wave (1, 2, 4)
+    int chunk_rows;               // rows per grid-z chunk: 64, or 32 (M split), or block_m (routed)
     // routed experts (MoE, routed != 0): workgroup chunk z covers the
     // 16 * MT padded route slots [z * 16 * MT, ...) of one expert
     // (block_expert[z]); a slot holds a route ordinal, or `routes` for

@@ -260,7 +260,7 @@ void gemm_kernel(GemmArgs a) {
     const int q = lane >> 4, col = lane & 15;
     const int tile0 = (blockIdx.x * kGemmWaves + wave) * J;
     const int split = blockIdx.y;
-    const int m0 = blockIdx.z * (a.routed ? 16 * MT : 64);
+    const int m0 = blockIdx.z * a.chunk_rows;
     // routed: this chunk's expert, or nothing to do past the routed blocks
     int expert = 0;
     if (a.routed) {
@@ -717,8 +717,8 @@ hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     // routed: one grid chunk per padded route block (a.m = block capacity)
     const int mt = a.routed ? a.block_m / 16 : (a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1));
-    const int rows_chunks = a.routed ? a.m / a.block_m : (a.m + 63) / 64;
-    const int mt_eff = a.routed || rows_chunks == 1 ? mt : 4;
+    const int rows_chunks = (a.m + a.chunk_rows - 1) / a.chunk_rows;
+    const int mt_eff = a.routed ? mt : (a.chunk_rows == 32 ? 2 : (rows_chunks == 1 ? mt : 4));
     const int j = a.tiles_per_wave;  // chosen by the host plan
     const int cols_per_block = kGemmWaves * j * 16;
     dim3 grid((a.n + cols_per_block - 1) / cols_per_block, a.split, rows_chunks);
