@@ -23,7 +23,7 @@
 
 #ifdef CUBIC_TIMELINE
 // Development instrumentation (never built into the shipped library).
-__device__ uint64_t g_acc_timeline[4096][16];
+__device__ uint64_t g_acc_timeline[4096][24];
 extern "C" __attribute__((visibility("default"))) int cubic_dev_acc_timeline(uint64_t* host) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_acc_timeline), sizeof(g_acc_timeline));
 }
@@ -75,22 +75,10 @@ __device__ __forceinline__ uint32_t key16_to_bf16(uint32_t k) {
 
 __device__ __forceinline__ bool nonfinite_bf16(uint32_t u) { return (u & 0x7F80u) == 0x7F80u; }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint32_t o = __shfl_xor(v, m);
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(v, m);
-        v = o > v ? o : v;
-    }
-    return v;
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -142,7 +130,7 @@ __device__ uint64_t wave_topk_u64(const uint64_t (&e)[P], int n_entries, int wan
     uint64_t lm = 0ull;
 #pragma unroll
     for (int q = 0; q < P; ++q) lm = e[q] > lm ? e[q] : lm;
-    const uint64_t tau = __shfl(wave_sort_desc_u64(lm, lane), want - 1);
+    const uint64_t tau = (uint64_t)readlane64((int64_t)wave_sort_desc_u64(lm, lane), want - 1);
     int mine = 0;
 #pragma unroll
     for (int q = 0; q < P; ++q) mine += (e[q] != 0ull && e[q] >= tau);
@@ -152,7 +140,7 @@ __device__ uint64_t wave_topk_u64(const uint64_t (&e)[P], int n_entries, int wan
         const int o = __shfl_up(incl, d);
         if (lane >= d) incl += o;
     }
-    const int total = __shfl(incl, kWave - 1);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (total <= kWave) {
         int pos = incl - mine;
 #pragma unroll
@@ -193,8 +181,14 @@ struct VerifyRow {
     int64_t draft;
     float temperature, top_p;
     int64_t top_k, seed, ordinal;
-    const float* uniforms;  // two floats or null
+    bool has_uniforms;      // explicit draws u0 (accept), u1 (resample); else Philox
+    float u0, u1;
     bool underfilled;
+    // staged: lane j < tp*k already holds candidate j of q, p0 and p1 (tp = 1;
+    // the pointers above are not read)
+    bool staged;
+    uint32_t st_q_s, st_p0_s, st_p1_s;
+    int64_t st_q_i, st_p0_i, st_p1_i;
 };
 
 template <int SLOTS>
@@ -227,7 +221,7 @@ __device__ __forceinline__ float vl_tree_sum(float (&x)[SLOTS], int block) {
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) x[s] = y[s];
     }
-    return __shfl(x[0], 0);
+    return lane_f32(x[0], 0);
 }
 
 template <int SLOTS>
@@ -238,7 +232,7 @@ __device__ __forceinline__ void vl_scan(float (&x)[SLOTS], int block, int lane) 
     for (int s = 0; s < SLOTS; ++s) x[s] = wave_row_scan(x[s]);
 #pragma unroll
     for (int s = 1; s < SLOTS; ++s)
-        if (kWave * s < block) x[s] = x[s] + __shfl(x[s - 1], kWave - 1);
+        if (kWave * s < block) x[s] = x[s] + lane_f32(x[s - 1], kWave - 1);
     (void)lane;
 }
 
@@ -248,14 +242,9 @@ __device__ __forceinline__ float vl_max(const float (&x)[SLOTS], int block) {
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) m = x[s] > m ? x[s] : m;  // NaN-ignoring
     (void)block;  // lanes past the block hold -inf
-    return __shfl(wave_max_f32(m), 0);
+    return lane_f32(wave_max_f32(m), 0);
 }
 
-__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
 
 __device__ __forceinline__ float readlanef(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -414,15 +403,23 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         const bool load_p = load && r.rows_ok;
         float qs = -__builtin_huge_valf(), p0s = qs, p1s = qs;
         int64_t qi = -1, p0i = -1, p1i = -1;
-        if (load) {
-            qs = bf16_bits_to_float(r.q_scores[rank * r.q_rank_stride + local]);
-            qi = r.q_ids[rank * r.q_rank_stride + local];
-        }
-        if (load_p) {
-            p0s = bf16_bits_to_float(r.p0_scores[rank * r.p_rank_stride + local]);
-            p0i = r.p0_ids[rank * r.p_rank_stride + local];
-            p1s = bf16_bits_to_float(r.p1_scores[rank * r.p_rank_stride + local]);
-            p1i = r.p1_ids[rank * r.p_rank_stride + local];
+        if (SLOTS == 1 && r.staged) {
+            if (load) { qs = bf16_bits_to_float(r.st_q_s); qi = r.st_q_i; }
+            if (load_p) {
+                p0s = bf16_bits_to_float(r.st_p0_s); p0i = r.st_p0_i;
+                p1s = bf16_bits_to_float(r.st_p1_s); p1i = r.st_p1_i;
+            }
+        } else {
+            if (load) {
+                qs = bf16_bits_to_float(r.q_scores[rank * r.q_rank_stride + local]);
+                qi = r.q_ids[rank * r.q_rank_stride + local];
+            }
+            if (load_p) {
+                p0s = bf16_bits_to_float(r.p0_scores[rank * r.p_rank_stride + local]);
+                p0i = r.p0_ids[rank * r.p_rank_stride + local];
+                p1s = bf16_bits_to_float(r.p1_scores[rank * r.p_rank_stride + local]);
+                p1i = r.p1_ids[rank * r.p_rank_stride + local];
+            }
         }
         const bool qr = cm && qi >= 0 && __builtin_fabsf(qs) < __builtin_huge_valf();
         const bool p0r = cm && p0i >= 0 && __builtin_fabsf(p0s) < __builtin_huge_valf();
@@ -437,16 +434,19 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         p1set.s[s] = p1s; p1set.i[s] = p1i; p1set.r[s] = v < block && p1r;
     }
     const bool pairs_valid = __all(lane_ok);
+    ACC_STAMP(16);
     LaneSet<SLOTS> q, p0, p1;
     const int qc = select_set<SLOTS>(qset, block, r.k, lane, sc, q);
     const int p0c = select_set<SLOTS>(p0set, block, r.k, lane, sc, p0);
     const int p1c = select_set<SLOTS>(p1set, block, r.k, lane, sc, p1);
 
+    ACC_STAMP(17);
     float qp[SLOTS], p0p[SLOTS], p1p[SLOTS], qm, p0m, p1m;
     probabilities<SLOTS>(q.s, r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
     probabilities<SLOTS>(p0.s, r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
     probabilities<SLOTS>(p1.s, r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
 
+    ACC_STAMP(18);
     float t1[SLOTS], t2[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
@@ -460,13 +460,14 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
     const float quotient = p_draft / q_draft;
     const float ratio = quotient < 1.0f ? quotient : 1.0f;
     const uint32_t key = (uint32_t)(r.seed ^ (r.seed >> 32) ^ 0x9E3779B9LL);
-    const float u_accept = r.uniforms ? r.uniforms[0] : philox_uniform(key, (uint32_t)(r.ordinal * 2));
+    const float u_accept = r.has_uniforms ? r.u0 : philox_uniform(key, (uint32_t)(r.ordinal * 2));
     const bool random_accepted = u_accept < ratio;
     const bool greedy = r.temperature == 0.0f;
-    const int64_t p0_top = __shfl(p0.i[0], 0), p1_top = __shfl(p1.i[0], 0);
+    const int64_t p0_top = readlane64(p0.i[0], 0), p1_top = readlane64(p1.i[0], 0);
     const bool greedy_accepted = r.draft == p0_top;
     const bool accepted = greedy ? greedy_accepted : random_accepted;
     wave_lds_sync();
+    ACC_STAMP(19);
 
     float q_at_p[SLOTS], residual[SLOTS];
 #pragma unroll
@@ -483,8 +484,9 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         residual[s] = d > 0.0f ? d : 0.0f;
         t1[s] = residual[s];
     }
+    ACC_STAMP(20);
     const float rmass = vl_tree_sum<SLOTS>(t1, block);
-    const float u_sample = r.uniforms ? r.uniforms[1]
+    const float u_sample = r.has_uniforms ? r.u1
                                       : philox_uniform(key ^ 0x85EBCA6Bu, (uint32_t)(r.ordinal * 2 + 1));
     float c1[SLOTS], cr[SLOTS];
 #pragma unroll
@@ -504,11 +506,12 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
     int64_t p1_token = kInt64Max, res_token = kInt64Max;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-        const int64_t a1 = __shfl(p1.i[s], p1_slot & (kWave - 1));
-        const int64_t ar = __shfl(p0.i[s], res_slot & (kWave - 1));
+        const int64_t a1 = readlane64(p1.i[s], p1_slot & (kWave - 1));
+        const int64_t ar = readlane64(p0.i[s], res_slot & (kWave - 1));
         if (p1_slot < block && p1_slot / kWave == s) p1_token = a1;
         if (res_slot < block && res_slot / kWave == s) res_token = ar;
     }
+    ACC_STAMP(21);
     const int64_t need = (greedy || r.underfilled) ? 1 : r.top_k;
     const bool valid = r.active && pairs_valid && r.rows_ok && r.temperature >= 0.0f &&
                        r.temperature < __builtin_huge_valf() && r.top_k >= 1 && r.top_k <= r.k &&
@@ -662,7 +665,7 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     const uint64_t hit = __ballot(retained[0] > target);
     const int sampled = hit ? __builtin_ctzll(hit) : kWave;
     const int chosen = greedy ? 0 : sampled;
-    const int64_t token = __shfl(sel_id, chosen & (kWave - 1));
+    const int64_t token = readlane64(sel_id, chosen & (kWave - 1));
     const bool valid = malformed == 0 && params_ok && enough &&
                        (greedy || (mass > 0.0f && sampled < kWave));
     ACC_STAMP(6);
@@ -701,7 +704,10 @@ __global__ __launch_bounds__(kWave) void verify_candidates_kernel(VerifyArgs a) 
     r.top_k = r.active ? a.top_ks[row] : 1;
     r.seed = r.active ? a.seeds[row] : 0;
     r.ordinal = r.active ? a.ordinals[row] : 0;
-    r.uniforms = a.uniforms ? a.uniforms + 2 * (int64_t)row : nullptr;
+    r.has_uniforms = a.uniforms != nullptr;
+    r.u0 = r.has_uniforms ? a.uniforms[2 * (int64_t)row] : 0.0f;
+    r.u1 = r.has_uniforms ? a.uniforms[2 * (int64_t)row + 1] : 0.0f;
+    r.staged = false;
     bool under = a.allow_underfilled != 0;
     if (a.constrained_rows) under = under && r.active && a.constrained_rows[row];
     r.underfilled = under;
@@ -743,6 +749,32 @@ struct TileScratch {
     int64_t decisions[8][2];
     uint64_t merge[kWaves][kWave];
 };
+
+// Inputs of one verified depth (proposal row pi of the fused verify), loaded
+// at kernel start by the wave that verifies it should its workgroup finish
+// the group: lane j < capacity holds the q candidate j.
+struct VerifyPrefetch {
+    uint32_t q_score;
+    int64_t q_id;
+    int64_t draft, top_k, seed, ordinal;
+    float temperature, top_p, u0, u1;
+};
+
+__device__ __forceinline__ VerifyPrefetch prefetch_verify(const AcceptArgs& a, int64_t pi, int lane) {
+    VerifyPrefetch p;
+    const bool in = lane < a.capacity;
+    p.q_score = in ? a.q_scores[pi * a.capacity + lane] : 0x7FC0u;
+    p.q_id = in ? a.q_ids[pi * a.capacity + lane] : -1;
+    p.draft = a.draft_tokens[pi];
+    p.temperature = a.temperatures[pi];
+    p.top_p = a.top_ps[pi];
+    p.top_k = a.top_ks[pi];
+    p.seed = a.seeds[pi];
+    p.ordinal = a.ordinals[pi];
+    p.u0 = a.uniforms ? a.uniforms[2 * pi] : 0.0f;
+    p.u1 = a.uniforms ? a.uniforms[2 * pi + 1] : 0.0f;
+    return p;
+}
 
 // Exact top-`kTop` composites of the lane-held elements of one wave.
 // keys are recomputed from the raw bf16 words (E chunks of 8 per lane).
@@ -869,6 +901,39 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
     return nonfinite != 0u;
 }
 
+// Greedy rows publish only their argmax: the tile keeps its single largest
+// composite (value desc, then lowest id; the composite order of tile_top) in
+// out_top[0] and zeros in the other slots.  Returns the non-finite flag as
+// tile_top does.
+template <int EMAX>
+__device__ bool tile_max(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
+                         int lane, uint32_t* out_top) {
+    uint32_t nonfinite = 0, best = 0;
+    const bool partial = chunks * kChunk > width_left;  // wave-uniform
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t word = (&raw[e].x)[w];
+            const uint32_t idx = base_idx + (uint32_t)(e * kChunk + 2 * w);  // low half's element
+            uint32_t valid = e < chunks ? 0xFFFFFFFFu : 0u;
+            if (partial)
+                valid &= ((int)idx < width_left ? 0x0000FFFFu : 0u) | ((int)idx + 1 < width_left ? 0xFFFF0000u : 0u);
+            const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
+            const u16x2_t inf = {0x7F80, 0x7F80};
+            nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
+            const uint32_t k2 = order_key16x2(word) & valid;
+            const uint32_t lo = k2 & 0xFFFFu, hi = k2 >> 16;  // 0 = empty element
+            const uint32_t c0 = lo ? (lo << 16) | (0xFFFFu - idx) : 0u;
+            const uint32_t c1 = hi ? (hi << 16) | (0xFFFEu - idx) : 0u;
+            const uint32_t c = c0 > c1 ? c0 : c1;
+            best = c > best ? c : best;
+        }
+    best = wave_max_u32(best);
+    if (lane < kTop) out_top[lane] = lane == 0 ? best : 0u;
+    return nonfinite != 0u;
+}
+
 template <int EMAX, bool FUSED, int SLOTS>
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __shared__ TileScratch ts;
@@ -903,11 +968,21 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) raw[e] = make_uint4(0, 0, 0, 0);
     }
+    // the fused verify's inputs for depth d = wave of this row's group, read
+    // now so that their latency hides under the tile phase (only the group's
+    // last workgroup uses them; deeper depths read them when verified)
+    const int group = row / a.group_rows;
+    VerifyPrefetch pre = {};
+    if (FUSED && wave < a.group_rows - 1) pre = prefetch_verify(a, (int64_t)wave * a.c + group, lane);
+    const bool greedy_row = a.row_temperatures[row] == 0.0f;  // row-uniform
     ACC_STAMP(1);
-    // wave top-kTop of this wave's share, then the workgroup's top-kTop
+    // wave top-kTop of this wave's share (the maximum alone for a greedy
+    // row), then the workgroup's top-kTop
     const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
-    const bool nonfinite = tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane,
-                                          wave, &ts.wave_top[wave * kTop]);
+    const bool nonfinite =
+        greedy_row ? tile_max<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, lane, &ts.wave_top[wave * kTop])
+                   : tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane, wave,
+                                    &ts.wave_top[wave * kTop]);
     const uint32_t bad = __any(nonfinite);
     if (lane == 0) ts.flags[wave] = bad;
     __syncthreads();
@@ -935,7 +1010,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                          ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3]);
     }
     // arrival: the last workgroup of this row group finalises it
-    const int group = row / a.group_rows;
     ACC_STAMP(3);
     if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) { ACC_STAMP(4); return; }
     ACC_STAMP(5);
@@ -948,28 +1022,45 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         uint32_t bad_row = 0;
         for (int t = lane; t < a.tiles; t += kWave) bad_row |= load_device(&a.partial_flags[(int64_t)r * a.tiles + t]);
         bad_row = __any(bad_row != 0);
-        // kTop global winners by (value desc, id asc) over tiles * kTop entries
-        constexpr int kPer = (kMaxTiles * kTop + kWave - 1) / kWave;
-        uint64_t entry[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int i = lane + q * kWave;
-            entry[q] = 0ull;
-            if (i < a.tiles * kTop) {
-                const uint32_t k32 = load_device(&a.partial_keys[(int64_t)r * a.tiles * kTop + i]);
-                if (k32 != 0u) {
-                    const uint32_t t = (uint32_t)(i / kTop);
-                    const uint32_t id = t * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
-                    entry[q] = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
-                }
-            }
-        }
-        if (gr == 0) ACC_STAMP(6);
-        const int want = a.count < kTop ? a.count : kTop;
-        const uint64_t my = wave_topk_u64<kPer>(entry, a.tiles * kTop, want, lane, ts.merge[wave]);
-        if (gr == 0) ACC_STAMP(7);
         const float temp = a.row_temperatures[r];
         const bool greedy_pub = temp == 0.0f;
+        const int want = a.count < kTop ? a.count : kTop;
+        uint64_t my = 0ull;
+        if (greedy_pub) {
+            // the tiles of a greedy row hold their maximum in slot 0: the
+            // row's argmax is the largest of those (lane 0 = rank 0)
+            uint64_t e = 0ull;
+            if (lane < a.tiles) {
+                const uint32_t k32 = load_device(&a.partial_keys[((int64_t)r * a.tiles + lane) * kTop]);
+                if (k32 != 0u) {
+                    const uint32_t id = (uint32_t)lane * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
+                    e = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
+                }
+            }
+            if (gr == 0) ACC_STAMP(6);
+            e = wave_max_u64(e);
+            my = lane == 0 ? e : 0ull;
+        } else {
+            // kTop global winners by (value desc, id asc) over tiles * kTop entries
+            constexpr int kPer = (kMaxTiles * kTop + kWave - 1) / kWave;
+            uint64_t entry[kPer];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                const int i = lane + q * kWave;
+                entry[q] = 0ull;
+                if (i < a.tiles * kTop) {
+                    const uint32_t k32 = load_device(&a.partial_keys[(int64_t)r * a.tiles * kTop + i]);
+                    if (k32 != 0u) {
+                        const uint32_t t = (uint32_t)(i / kTop);
+                        const uint32_t id = t * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
+                        entry[q] = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
+                    }
+                }
+            }
+            if (gr == 0) ACC_STAMP(6);
+            my = wave_topk_u64<kPer>(entry, a.tiles * kTop, want, lane, ts.merge[wave]);
+        }
+        if (gr == 0) ACC_STAMP(7);
         const int j = lane;  // capacity <= 64
         if (j < a.capacity) {
             uint16_t sc = 0x7FC0u;
@@ -1008,6 +1099,17 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         VerifyRow vr;
         vr.active = c < a.live_rows;
         vr.rows_ok = true;
+        const bool prefetched = d == wave;  // first depth of this wave
+        // candidates into registers: q from the prefetch (or global), the
+        // target rows d and d + 1 from LDS
+        const bool in = lane < a.capacity;
+        vr.staged = true;
+        vr.st_q_s = prefetched ? pre.q_score : (in ? (uint32_t)a.q_scores[pi * a.capacity + lane] : 0x7FC0u);
+        vr.st_q_i = prefetched ? pre.q_id : (in ? a.q_ids[pi * a.capacity + lane] : -1);
+        vr.st_p0_s = ts.cand_score[d][lane];
+        vr.st_p0_i = ts.cand_id[d][lane];
+        vr.st_p1_s = ts.cand_score[d + 1][lane];
+        vr.st_p1_i = ts.cand_id[d + 1][lane];
         vr.q_scores = a.q_scores + pi * a.capacity;
         vr.q_ids = a.q_ids + pi * a.capacity;
         vr.p0_scores = ts.cand_score[d];
@@ -1019,13 +1121,26 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         vr.tp = 1;
         vr.k = a.capacity;
         vr.block = a.block;
-        vr.draft = vr.active ? a.draft_tokens[pi] : -1;
-        vr.temperature = vr.active ? a.temperatures[pi] : 1.0f;
-        vr.top_p = vr.active ? a.top_ps[pi] : 1.0f;
-        vr.top_k = vr.active ? a.top_ks[pi] : 1;
-        vr.seed = vr.active ? a.seeds[pi] : 0;
-        vr.ordinal = vr.active ? a.ordinals[pi] : 0;
-        vr.uniforms = a.uniforms ? a.uniforms + 2 * pi : nullptr;
+        if (prefetched) {
+            vr.draft = vr.active ? pre.draft : -1;
+            vr.temperature = vr.active ? pre.temperature : 1.0f;
+            vr.top_p = vr.active ? pre.top_p : 1.0f;
+            vr.top_k = vr.active ? pre.top_k : 1;
+            vr.seed = vr.active ? pre.seed : 0;
+            vr.ordinal = vr.active ? pre.ordinal : 0;
+            vr.u0 = pre.u0;
+            vr.u1 = pre.u1;
+        } else {
+            vr.draft = vr.active ? a.draft_tokens[pi] : -1;
+            vr.temperature = vr.active ? a.temperatures[pi] : 1.0f;
+            vr.top_p = vr.active ? a.top_ps[pi] : 1.0f;
+            vr.top_k = vr.active ? a.top_ks[pi] : 1;
+            vr.seed = vr.active ? a.seeds[pi] : 0;
+            vr.ordinal = vr.active ? a.ordinals[pi] : 0;
+            vr.u0 = a.uniforms ? a.uniforms[2 * pi] : 0.0f;
+            vr.u1 = a.uniforms ? a.uniforms[2 * pi + 1] : 0.0f;
+        }
+        vr.has_uniforms = a.uniforms != nullptr;
         vr.underfilled = false;
         verify_wave<SLOTS>(vr, vs[wave], lane, ts.decisions[d]);
         if (lane == 0) {

@@ -157,7 +157,10 @@ struct TilePlan {
 
 bool plan_tiles(int rows, int width, TilePlan* out) {
     if (width <= 0 || rows <= 0) return false;
-    int target = (int)ceil_div(1024, rows);
+#ifndef CUBIC_TILE_TARGET
+#define CUBIC_TILE_TARGET 512
+#endif
+    int target = (int)ceil_div(CUBIC_TILE_TARGET, rows);
     if (target < 1) target = 1;
     if (target > kMaxTiles) target = kMaxTiles;
     int64_t tw = ceil_div(ceil_div(width, target), kChunk) * kChunk;

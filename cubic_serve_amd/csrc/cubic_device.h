@@ -155,13 +155,37 @@ __device__ __forceinline__ float dpp_or_zero(float x) {
 // m = 4 and m = 8 read the half-row / row mirror: after the steps below m
 // every lane of a quad (of an 8-group) holds the same value, so the mirror
 // lane's value is the xor partner's.
+// m = 16 and m = 32 use the gfx950 lane swaps: v_permlane16_swap exchanges the
+// odd 16-lane rows of its first operand with the even rows of its second, and
+// v_permlane32_swap the upper half of the first with the lower half of the
+// second.  With x in both operands, lane i then holds {x[i], x[i ^ m]} in the
+// two results, in an order that depends on i; IEEE addition is commutative, so
+// their sum is x[i] + x[i ^ m] bit for bit.
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// x[i ^ 16] / x[i ^ 32] (lanes whose bit m is clear take the second result).
+__device__ __forceinline__ uint32_t xor16_u32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t xor32_u32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+}
+
 __device__ __forceinline__ float wave_butterfly_sum(float x, int width) {
     if (width > 1) x = x + dpp_or_zero<0xB1>(x);
     if (width > 2) x = x + dpp_or_zero<0x4E>(x);
     if (width > 4) x = x + dpp_or_zero<0x141>(x);
     if (width > 8) x = x + dpp_or_zero<0x140>(x);
-    if (width > 16) x = x + __shfl_xor(x, 16);
-    if (width > 32) x = x + __shfl_xor(x, 32);
+    if (width > 16) x = xor16_sum(x);
+    if (width > 32) x = xor32_sum(x);
     return x;
 }
 
@@ -172,9 +196,43 @@ __device__ __forceinline__ float wave_max_f32(float x) {
     o = dpp_or_zero<0x4E>(x); x = o > x ? o : x;
     o = dpp_or_zero<0x141>(x); x = o > x ? o : x;
     o = dpp_or_zero<0x140>(x); x = o > x ? o : x;
-    o = __shfl_xor(x, 16); x = o > x ? o : x;
-    o = __shfl_xor(x, 32); x = o > x ? o : x;
+    o = __uint_as_float(xor16_u32(__float_as_uint(x))); x = o > x ? o : x;
+    o = __uint_as_float(xor32_u32(__float_as_uint(x))); x = o > x ? o : x;
     return x;
+}
+
+// Maxima over the 64 lanes of unsigned keys (every lane ends with the maximum).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    uint32_t o;
+    o = dpp_u32<0xB1>(v); v = o > v ? o : v;
+    o = dpp_u32<0x4E>(v); v = o > v ? o : v;
+    o = dpp_u32<0x141>(v); v = o > v ? o : v;
+    o = dpp_u32<0x140>(v); v = o > v ? o : v;
+    o = xor16_u32(v); v = o > v ? o : v;
+    o = xor32_u32(v); v = o > v ? o : v;
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    auto step = [&](uint32_t olo, uint32_t ohi) {
+        const uint64_t o = ((uint64_t)ohi << 32) | olo;
+        v = o > v ? o : v;
+    };
+    step(dpp_u32<0xB1>((uint32_t)v), dpp_u32<0xB1>((uint32_t)(v >> 32)));
+    step(dpp_u32<0x4E>((uint32_t)v), dpp_u32<0x4E>((uint32_t)(v >> 32)));
+    step(dpp_u32<0x141>((uint32_t)v), dpp_u32<0x141>((uint32_t)(v >> 32)));
+    step(dpp_u32<0x140>((uint32_t)v), dpp_u32<0x140>((uint32_t)(v >> 32)));
+    step(xor16_u32((uint32_t)v), xor16_u32((uint32_t)(v >> 32)));
+    step(xor32_u32((uint32_t)v), xor32_u32((uint32_t)(v >> 32)));
+    return v;
+}
+
+// Value of lane l (wave-uniform l) without a cross-lane permute.
+__device__ __forceinline__ float lane_f32(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 // Inclusive scan over the 64 lanes: inside each 16-lane row x[i] += x[i - d]

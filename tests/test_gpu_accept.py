@@ -49,6 +49,14 @@ def test_candidates_match_oracle(oracle, rows, width):
     bits[0, 18] = np.uint16(0x0000)
     if rows > 2:
         bits[2, width // 2] = np.uint16(0x7FC0)  # NaN row -> id -2
+    # greedy row 1: a tie for the maximum across tiles (lowest id wins)
+    bits[1, 7] = bits[1, width - 2] = np.uint16(0x4300)
+    if rows > 4:
+        # greedy row 4: every value negative but a -0 (id 100) and a +0 (id
+        # width - 5); -0 == +0, so the lower id and its own bits are published
+        bits[4] = bits[4] | np.uint16(0x8000)
+        bits[4, 100] = np.uint16(0x8000)
+        bits[4, width - 5] = np.uint16(0x0000)
     temps = np.array([(0.0 if r % 3 == 1 else 0.7) for r in range(rows)], np.float32)
     owned = max(1, rows - 1)
     count, capacity = 20, 24
@@ -263,3 +271,10 @@ def test_fused_stochastic_cfg3_shape(oracle):
 def test_fused_small_shapes_and_dead_rows(oracle, use_uniforms):
     _fused_case(oracle, 5, 2, 3000, True, 11, use_uniforms=use_uniforms, live=3)
     _fused_case(oracle, 1, 1, 32768, False, 12)
+
+
+@pytest.mark.parametrize("stochastic", [True, False])
+def test_fused_deep_drafts(oracle, stochastic):
+    """k = 5 drafts: depths past the fourth are verified on a second pass of
+    the waves, reading their inputs directly rather than from the prefetch."""
+    _fused_case(oracle, 3, 5, 5000, stochastic, 13, live=2)
