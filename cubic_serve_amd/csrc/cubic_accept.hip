@@ -93,7 +93,7 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane) {
     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-            const uint32_t o = __shfl_xor(v, stride);
+            const uint32_t o = xor_lane_rt(v, stride);  // stride is a constant once unrolled
             const bool upper = (lane & stride) != 0;
             const bool desc = (lane & size) == 0;
             const uint32_t hi = o > v ? o : v, lo = o > v ? v : o;
@@ -109,7 +109,7 @@ __device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v, int lane) {
     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-            const uint64_t o = __shfl_xor(v, stride);
+            const uint64_t o = xor_lane_rt(v, stride);  // stride is a constant once unrolled
             const bool upper = (lane & stride) != 0;
             const bool desc = (lane & size) == 0;
             const uint64_t hi = o > v ? o : v, lo = o > v ? v : o;
@@ -134,12 +134,14 @@ __device__ uint64_t wave_topk_u64(const uint64_t (&e)[P], int n_entries, int wan
     int mine = 0;
 #pragma unroll
     for (int q = 0; q < P; ++q) mine += (e[q] != 0ull && e[q] >= tau);
+    // inclusive prefix count: the row-wise DPP scan of wave_row_scan on integers
     int incl = mine;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-    }
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, false);
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, false);
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, false);
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, false);
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);
+    incl += (int)__builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);
     const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (total <= kWave) {
         int pos = incl - mine;
@@ -791,7 +793,7 @@ __device__ __forceinline__ uint32_t elem_composite(const uint4 (&raw)[EMAX], int
 // Returns whether any element of the lane's share is non-finite.
 template <int EMAX>
 __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
-                         TileScratch& ts, int lane, int wave, uint32_t* out_top) {
+                         TileScratch& ts, uint32_t* kw, int lane, int wave, uint32_t* out_top) {
     // 1. order keys, two per word (elements 2w, 2w + 1 of a chunk), 0 = empty;
     //    a half is non-finite iff its magnitude is >= 0x7F80
     uint32_t key2[EMAX][4];
@@ -833,31 +835,45 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
     }
     const uint32_t thr = tau > 0u ? tau : 1u;  // empty elements never survive
     ACC_STAMP(12);
-    // 3. compact survivors (key >= thr) as composites, in element order; words
-    //    without a survivor in any lane are skipped with one wave-wide test
-    uint32_t total = 0;  // wave-uniform
-    const u16x2_t thr2 = {(unsigned short)thr, (unsigned short)thr};
+    // 3. compact survivors (key >= thr) as composites.  Each lane marks the
+    //    words holding a survivor (saturating packed subtract: nonzero iff a
+    //    half is >= thr) and spills its keys to LDS word-major (lane-distinct
+    //    banks); the wave then takes one marked word per lane per round, so
+    //    the rounds number the largest per-lane count of marked words, not
+    //    the words.  Survivor order is irrelevant: ranks count composites.
+    static_assert(EMAX * 4 <= 64, "word mask");
+    uint64_t marks = 0;
+    const u16x2_t thr_m1 = {(unsigned short)(thr - 1u), (unsigned short)(thr - 1u)};
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const uint32_t k2 = key2[e][w];
-            const uint32_t hit =
-                __builtin_bit_cast(uint32_t, (i16x2_t)(__builtin_bit_cast(u16x2_t, k2) >= thr2));
-            if (!__ballot(hit != 0u)) continue;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t k = h ? k2 >> 16 : k2 & 0xFFFFu;
-                const uint64_t m = __ballot(k >= thr);
-                if (m) {
-                    const uint32_t pos = total + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-                    const uint32_t idx = base_idx + (uint32_t)(e * kChunk + 2 * w + h);
-                    if (k >= thr && pos < kWave) ts.survivors[wave][pos] = (k << 16) | (0xFFFFu - idx);
-                    total += (uint32_t)__popcll(m);
-                }
-            }
+            const uint32_t d = __builtin_bit_cast(
+                uint32_t, (u16x2_t)__builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2_t, k2), thr_m1));
+            marks |= (uint64_t)(d != 0u) << (e * 4 + w);
+            kw[(e * 4 + w) * kWave + lane] = k2;
         }
+    wave_lds_sync();
+    uint32_t total = 0;  // wave-uniform
+    while (__ballot(marks != 0ull)) {
+        const bool has = marks != 0ull;
+        const int i = has ? (int)__builtin_ctzll(marks) : 0;
+        marks &= marks - 1ull;
+        const uint32_t k2 = kw[i * kWave + lane];
+        const uint32_t idx0 = base_idx + (uint32_t)((i >> 2) * kChunk + 2 * (i & 3));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t k = h ? k2 >> 16 : k2 & 0xFFFFu;
+            const bool sv = has && k >= thr;
+            const uint64_t m = __ballot(sv);
+            const uint32_t pos = total + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (sv && pos < kWave) ts.survivors[wave][pos] = (k << 16) | (0xFFFFu - (idx0 + (uint32_t)h));
+            total += (uint32_t)__popcll(m);
+        }
+    }
+    wave_lds_sync();  // the spill is rewritten by this wave's next tile only
     ACC_STAMP(13);
     if (lane < kTop) out_top[lane] = 0u;
     if (total <= kWave) {
@@ -938,6 +954,7 @@ template <int EMAX, bool FUSED, int SLOTS>
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __shared__ TileScratch ts;
     __shared__ VerifyScratch<SLOTS> vs[kWaves];
+    __shared__ uint32_t key_spill[kWaves * EMAX * 4 * kWave];  // tile_top's key words, word-major
     const int tile = blockIdx.x, row = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const bool owned = row < a.owned_rows;
@@ -981,8 +998,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
     const bool nonfinite =
         greedy_row ? tile_max<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, lane, &ts.wave_top[wave * kTop])
-                   : tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts, lane, wave,
-                                    &ts.wave_top[wave * kTop]);
+                   : tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts,
+                                    &key_spill[wave * EMAX * 4 * kWave], lane, wave, &ts.wave_top[wave * kTop]);
     const uint32_t bad = __any(nonfinite);
     if (lane == 0) ts.flags[wave] = bad;
     __syncthreads();

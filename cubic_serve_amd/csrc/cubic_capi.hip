@@ -69,7 +69,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
         while (split < 8 && (ceil_div(p.k_blocks, split) > 16 || out_blocks * split < 256)) split *= 2;
         if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
     }
-#ifdef CUBIC_TIMELINE  // instrumented build only: plan overrides for sweeps
+#if defined(CUBIC_TIMELINE) || defined(CUBIC_DEV_PLAN)  // instrumented builds only: plan overrides for sweeps
     if (const char* e = getenv("CUBIC_DEV_J")) p.tiles_per_wave = atoi(e);
     if (const char* e = getenv("CUBIC_DEV_SPLIT")) split = atoi(e);
 #endif
@@ -81,7 +81,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
     p.chunk_rows = 64;
     if (p.tiles_per_wave == 1 && m > 32 && m <= 64 && (int64_t)p.col_blocks * split < 512)
         p.chunk_rows = 32;
-#ifdef CUBIC_TIMELINE
+#if defined(CUBIC_TIMELINE) || defined(CUBIC_DEV_PLAN)
     if (const char* e = getenv("CUBIC_DEV_MSPLIT")) p.chunk_rows = atoi(e) && m > 32 && m <= 64 ? 32 : 64;
 #endif
     p.blocks_per_split = (int)ceil_div(p.k_blocks, split);

@@ -230,6 +230,49 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// x[i ^ M] for M = 1, 2, 4, ..., 32 without an LDS permute: quad_perm for 1
+// and 2; for 4 and 8 the lanes whose bit M is set take row_shr:M (lane i - M)
+// and the others row_shl:M (lane i + M); the lane swaps for 16 and 32.
+// Callers keep every lane of the wave active.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 1) return dpp_u32<0xB1>(v);
+    else if constexpr (M == 2) return dpp_u32<0x4E>(v);
+    else if constexpr (M == 4 || M == 8) {
+        // both reads with every lane active (a read from a lane disabled by a
+        // branch returns 0), then a bitwise blend rather than a select
+        const uint32_t down = dpp_u32<0x110 + M>(v), up = dpp_u32<0x100 + M>(v);
+        const uint32_t m = 0u - ((__lane_id() >> (M == 4 ? 2 : 3)) & 1u);
+        return (down & m) | (up & ~m);
+    }
+    else if constexpr (M == 16) return xor16_u32(v);
+    else return xor32_u32(v);
+}
+template <int M>
+__device__ __forceinline__ uint64_t xor_lane(uint64_t v) {
+    return ((uint64_t)xor_lane<M>((uint32_t)(v >> 32)) << 32) | xor_lane<M>((uint32_t)v);
+}
+__device__ __forceinline__ uint32_t xor_lane_rt(uint32_t v, int m) {
+    switch (m) {
+        case 1: return xor_lane<1>(v);
+        case 2: return xor_lane<2>(v);
+        case 4: return xor_lane<4>(v);
+        case 8: return xor_lane<8>(v);
+        case 16: return xor_lane<16>(v);
+        default: return xor_lane<32>(v);
+    }
+}
+__device__ __forceinline__ uint64_t xor_lane_rt(uint64_t v, int m) {
+    switch (m) {
+        case 1: return xor_lane<1>(v);
+        case 2: return xor_lane<2>(v);
+        case 4: return xor_lane<4>(v);
+        case 8: return xor_lane<8>(v);
+        case 16: return xor_lane<16>(v);
+        default: return xor_lane<32>(v);
+    }
+}
+
 // Value of lane l (wave-uniform l) without a cross-lane permute.
 __device__ __forceinline__ float lane_f32(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
