@@ -965,8 +965,16 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
 
     ACC_STAMP(0);
     uint4 raw[EMAX];
-    if (owned) {
-        const bool vec = a.vector_loads != 0;
+    const bool vec = a.vector_loads != 0;
+    if (owned && vec && chunks * kChunk <= width_left) {
+        // every chunk complete: all loads in one straight run so that they are
+        // in flight together (per-chunk branches made the compiler wait for
+        // each load before issuing the next); chunks past the tile repeat the
+        // last one and are masked out by the tile reductions (e >= chunks)
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+            raw[e] = *reinterpret_cast<const uint4*>(src + (e < chunks ? e : chunks - 1) * kChunk + threadIdx.x * 8);
+    } else if (owned) {
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) {
             raw[e] = make_uint4(0, 0, 0, 0);
