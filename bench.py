@@ -230,6 +230,7 @@ def measure_extras() -> dict:
     256 rows (T 0.8, top-p 0.9, top-k 20).
     checkpoint: one Qwen3-8B-shaped layer loaded from safetensors and
     repacked for the GEMM (measure_checkpoint).
+    cfg5: Llama-3-70B-shaped layers, bits x M sweep (measure_cfg5).
     Times are per launch (HIP events, graph replays); GB/s use the
     algorithmic bytes of each launch.
     """
@@ -347,6 +348,52 @@ def measure_extras() -> dict:
         root[f"c{rows}_us"] = round(ms * 1e3, 2)
     out["root_sampler"] = root
     out["checkpoint"] = measure_checkpoint(dev)
+    out["cfg5"] = measure_cfg5(dev)
+    return out
+
+
+def measure_cfg5(dev) -> dict:
+    """Llama-3-70B-shaped layer linears (qkv 8192 -> 10240,
+    o 8192 -> 8192, gate/up 8192 -> 2 x 28672 as one grouped launch, down
+    28672 -> 8192), Cubic bits in {2, 3, 4, 6, 8}, group 128, weights N(0, 0.02)
+    quantized on the GPU, bf16 activations N(0, 1), M in {1, 8, 64, 512}.
+    One layer (285-622 MB of weights, more than the 256 MB Infinity Cache)
+    is captured in one HIP graph; per (bits, M): layer us, algorithmic GB/s
+    and TFLOP/s over its four launches."""
+    import torch
+
+    from cubic_serve_amd import linear, quantization as qz
+
+    hidden, qkv, inter = 8192, 10240, 28672
+    shapes = ((qkv, hidden), (hidden, hidden), (2 * inter, hidden), (hidden, inter))
+    g = torch.Generator(device=dev).manual_seed(50)
+    out = {}
+    for bits in (2, 3, 4, 6, 8):
+        def prep(n, k):
+            w = torch.randn((n, k), generator=g, device=dev) * 0.02
+            m = qz.quantize_cubic(w, bits=bits, group_in=GROUP)
+            del w
+            return linear.prepare_matrix(m, dev)
+        w_qkv, w_o, w_down = prep(qkv, hidden), prep(hidden, hidden), prep(hidden, inter)
+        w_gate, w_up = prep(inter, hidden), prep(inter, hidden)
+        w_gu = linear.PreparedCubic(torch.cat([w_gate.codes, w_up.codes]), torch.cat([w_gate.meta, w_up.meta]),
+                                    2 * inter, hidden, bits, GROUP)
+        del w_gate, w_up
+        for m in (1, 8, 64, 512):
+            x = torch.randn((m, hidden), generator=g, device=dev).to(torch.bfloat16)
+            xd = torch.randn((m, inter), generator=g, device=dev).to(torch.bfloat16)
+            ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for n in (qkv, hidden, inter, inter, hidden)]
+            binds = [linear.bind_prepared(x, w_qkv, (ys[0],)), linear.bind_prepared(x, w_o, (ys[1],)),
+                     linear.bind_prepared(x, w_gu, (ys[2], ys[3]), (inter, inter)),
+                     linear.bind_prepared(xd, w_down, (ys[4],))]
+            ms = time_graph(capture(lambda: [b.launch() for b in binds]), 10, 3)
+            nbytes = sum(gemm_bytes(m, n, k, bits) for n, k in shapes)
+            flops = sum(2 * m * n * k for n, k in shapes)
+            out[f"w{bits}_m{m}"] = {"layer_us": round(ms * 1e3, 1), "gbs": round(nbytes / ms / 1e6, 1),
+                                    "tflops": round(flops / ms / 1e9, 1)}
+            del binds, ys, x, xd
+        del w_qkv, w_o, w_down, w_gu
+        torch.cuda.empty_cache()
     return out
 
 

@@ -209,3 +209,48 @@ def test_wide_output_repeatable_and_row_invariant(oracle):
     for mrows in (1, 2, 17, 33):
         y = ops.linear(x[:mrows].contiguous(), m)
         assert torch.equal(y, first[:mrows]), mrows
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_llama70b_cfg5_shapes_sampled_enclosure(oracle, bits):
+    """Llama-3-70B layer linears (qkv 8192 -> 10240, o
+    8192 -> 8192, gate/up 8192 -> 2 x 28672 as one grouped launch, down
+    28672 -> 8192), weights N(0, 0.02), at M = 1, 8, 64, 512: every sampled
+    output inside the FP64 enclosure (64 columns per linear at a position that
+    moves with M; at M = 512 the first and last 64-row chunks), and a row's
+    output equal for M = 1, 8 and 64 (one 64-row chunk)."""
+    print(f"cfg5 bits={bits}", flush=True)
+    hidden, qkv, inter = 8192, 10240, 28672
+    g = torch.Generator(device=DEV).manual_seed(100 + bits)
+
+    def quant(n, k):
+        w = torch.randn((n, k), generator=g, device=DEV) * 0.02
+        m = qz.quantize_cubic(w, bits=bits, group_in=128)
+        del w
+        return m
+
+    ops = linear.PackedLinearOperators()
+    mats = {"qkv": quant(qkv, hidden), "o": quant(hidden, hidden), "down": quant(hidden, inter)}
+    gate, up = quant(inter, hidden), quant(inter, hidden)
+    for mi, mrows in enumerate((1, 8, 64, 512)):
+        x = torch.randn((mrows, hidden), generator=g, device=DEV).to(torch.bfloat16)
+        xd = torch.randn((mrows, inter), generator=g, device=DEV).to(torch.bfloat16)
+        row_sets = [slice(0, mrows)] if mrows <= 64 else [slice(0, 64), slice(mrows - 64, mrows)]
+        outs = {name: ops.linear(xd if name == "down" else x, m) for name, m in mats.items()}
+        yg = torch.empty((mrows, inter), dtype=torch.bfloat16, device=DEV)
+        yu = torch.empty((mrows, inter), dtype=torch.bfloat16, device=DEV)
+        ops.bind_linear_group(x, (gate, up), (yg, yu)).launch()
+        torch.cuda.synchronize()
+        checks = [(m, xd if name == "down" else x, outs[name]) for name, m in mats.items()]
+        checks += [(gate, x, yg), (up, x, yu)]
+        for m, xin, y in checks:
+            n = m.shape[0]
+            start = (mi * 1237 * 16) % (n - 64)
+            part = m.rows(start, start + 64).to("cpu")
+            for rows in row_sets:
+                _check_linear(oracle, part, xin[rows].contiguous(), y[rows, start:start + 64].contiguous())
+        if mrows == 64:
+            for name, m in mats.items():
+                xin = xd if name == "down" else x
+                for sub in (1, 8):
+                    assert torch.equal(ops.linear(xin[:sub].contiguous(), m), outs[name][:sub]), (name, sub)
