@@ -171,6 +171,23 @@ __device__ __forceinline__ uint4 direct_fragment(const uint32_t* w, int f, float
     return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
+// bits 5..7 with one metadata group per k-block: the group's bf16 levels of
+// the lane's column sit in LDS (lv, indexed by magnitude); a weight is a
+// lookup plus the stored sign, bit for bit what direct_fragment computes.
+template <int BITS>
+__device__ __forceinline__ uint4 table_fragment(const uint32_t* w, int f, const uint16_t* lv) {
+    constexpr uint32_t kMagMask = (1u << (BITS - 1)) - 1u;
+    uint32_t out[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const uint32_t c0 = code_at<BITS>(w, 8 * f + 2 * h), c1 = code_at<BITS>(w, 8 * f + 2 * h + 1);
+        const uint32_t l0 = lv[c0 & kMagMask], l1 = lv[c1 & kMagMask];
+        const uint32_t sg = ((c0 >> (BITS - 1)) << 15) | ((c1 >> (BITS - 1)) << 31);
+        out[h] = (l0 | (l1 << 16)) ^ sg;
+    }
+    return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 // ---------------------------------------------------------------------------
 // GEMM kernel
 //   grid.x: column blocks of kGemmWaves waves x J tiles x 16 columns
@@ -255,6 +272,14 @@ void gemm_kernel(GemmArgs a) {
     constexpr int S = Stages<BITS, J>::value;
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
     __shared__ float t_lds[128];
+    // bits 5..7, G128: per wave, the bf16 levels of its J x 16 columns for the
+    // current k-block's group (wave-private, rebuilt every k-block)
+    constexpr bool LT = G128 && BITS >= 5 && BITS <= 7;
+    constexpr int NM = 1 << (BITS - 1);
+    // rows padded by 4 levels (8 bytes): 16 columns' rows start on 16 distinct
+    // bank groups instead of 4, and stay 8-byte aligned for the pair writes
+    constexpr int NMP = NM + 4;
+    __shared__ __attribute__((aligned(16))) uint16_t lv_lds[LT ? kGemmWaves * J * 16 * NMP : 1];
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int q = lane >> 4, col = lane & 15;
@@ -413,6 +438,29 @@ void gemm_kernel(GemmArgs a) {
                     mb[j] = half_bits_to_float(meta[j][1] >> 16);
                 }
             }
+            if constexpr (LT) {
+                // the four lanes of a column (quarters q) evaluate a quarter of
+                // its levels each, rounded as direct_fragment rounds them
+                constexpr int kPer = NM / 4;
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    uint32_t pairs[kPer / 2];
+#pragma unroll
+                    for (int p = 0; p < kPer / 2; ++p) {
+                        const int m = q * kPer + 2 * p;
+                        pairs[p] = pack_bf16x2(curve_level(t_lds[m], ms[j], ma[j], mb[j]),
+                                               curve_level(t_lds[m + 1], ms[j], ma[j], mb[j]));
+                    }
+                    uint32_t* dst = reinterpret_cast<uint32_t*>(&lv_lds[((wave * J + j) * 16 + col) * NMP + q * kPer]);
+#pragma unroll
+                    for (int p = 0; p < kPer / 2; p += 2)
+                        *reinterpret_cast<uint2*>(dst + p) = make_uint2(pairs[p], pairs[p + 1]);
+                }
+                // every lane reads the levels its column's other lanes wrote
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
 
             // fragment f of lane (col, q): chunk 4q + f of row col in each 16-row block
             auto afrag_at = [&](int mt, int f) {
@@ -436,6 +484,8 @@ void gemm_kernel(GemmArgs a) {
                     uint4 bw;
                     if constexpr (BITS <= 4)
                         bw = decode_fragment<BITS>(codes[j], f, tab[j]);
+                    else if constexpr (LT)
+                        bw = table_fragment<BITS>(codes[j], f, &lv_lds[((wave * J + j) * 16 + col) * NMP]);
                     else
                         bw = direct_fragment<BITS>(codes[j], f, ms[j], ma[j], mb[j], t_lds);
                     const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
