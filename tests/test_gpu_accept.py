@@ -37,7 +37,7 @@ def cuda(values, dtype):
 # --------------------------------------------------------------------------- #
 # candidates
 # --------------------------------------------------------------------------- #
-@pytest.mark.parametrize("rows,width", [(3, 300), (2, 32768), (64, 151936), (5, 70001)])
+@pytest.mark.parametrize("rows,width", [(3, 300), (2, 32768), (64, 151936), (5, 70001), (2, 400003)])
 def test_candidates_match_oracle(oracle, rows, width):
     print(f"candidates rows={rows} width={width}", flush=True)
     g = torch.Generator().manual_seed(rows * 7 + width)
@@ -271,6 +271,13 @@ def test_fused_stochastic_cfg3_shape(oracle):
 def test_fused_small_shapes_and_dead_rows(oracle, use_uniforms):
     _fused_case(oracle, 5, 2, 3000, True, 11, use_uniforms=use_uniforms, live=3)
     _fused_case(oracle, 1, 1, 32768, False, 12)
+
+
+@pytest.mark.parametrize("stochastic", [True, False])
+def test_fused_wide_vocabulary(oracle, stochastic):
+    """A vocabulary past 24 tiles of 8 chunks (393216): tiles of up to 16
+    chunks per thread, the largest tile-phase variant."""
+    _fused_case(oracle, 2, 1, 400003, stochastic, 21)
 
 
 @pytest.mark.parametrize("stochastic", [True, False])

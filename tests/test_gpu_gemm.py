@@ -86,6 +86,21 @@ def test_identity_contraction_is_exact_decode(oracle, bits, fmt):
     assert np.array_equal(canon_zero(got), canon_zero(want))
 
 
+@pytest.mark.parametrize("bits", [5, 6, 7])
+@pytest.mark.parametrize("gi", [128, 256])
+@pytest.mark.parametrize("fmt", FMTS)
+def test_identity_level_table_bits_exact(oracle, bits, gi, fmt):
+    """5-7 bits with groups of whole k-blocks decode through per-k-block level
+    tables in LDS: every code's output equals bf16(decode_cubic), including a
+    group that spans two k-blocks and a K tail."""
+    n, k = 40, 600  # 4 whole k-blocks and a tail of 88
+    m = random_matrix(n, k, bits, gi, fmt, seed=bits * 100 + gi + FMTS.index(fmt), partitions=(24, 16))
+    x = torch.eye(k, dtype=torch.bfloat16, device=DEV)
+    y = linear.PackedLinearOperators().linear(x, m.to(DEV))
+    got = to_bits(y.T.contiguous())
+    assert np.array_equal(canon_zero(got), canon_zero(oracle_decode_bits(oracle, m)))
+
+
 @pytest.mark.parametrize("k,gi", [(200, 32), (384, 256), (136, 128)])
 def test_identity_partial_groups_and_k_tails(oracle, k, gi):
     m = random_matrix(33, k, 4, gi, qz.FMT_F32, seed=k)
