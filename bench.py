@@ -231,6 +231,8 @@ def measure_extras() -> dict:
     checkpoint: one Qwen3-8B-shaped layer loaded from safetensors and
     repacked for the GEMM (measure_checkpoint).
     cfg5: Llama-3-70B-shaped layers, bits x M sweep (measure_cfg5).
+    cfg1: the CPU-runnable configuration's lm_head (M = 2) and greedy
+    acceptance on the GPU (measure_cfg1).
     Times are per launch (HIP events, graph replays); GB/s use the
     algorithmic bytes of each launch.
     """
@@ -241,6 +243,8 @@ def measure_extras() -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(20)
     out = {}
+    # ---- cfg1 --------------------------------------------------------------
+    out["cfg1"] = measure_cfg1(dev)
     # ---- cfg3 --------------------------------------------------------------
     c, depth, rows = 64, 3, 64 * 4
     w = torch.randn((VOCAB, HIDDEN), generator=g, device=dev) * 0.02
@@ -350,6 +354,54 @@ def measure_extras() -> dict:
     out["checkpoint"] = measure_checkpoint(dev)
     out["cfg5"] = measure_cfg5(dev)
     return out
+
+
+def measure_cfg1(dev) -> dict:
+    """BASELINE config 1 on the GPU: lm_head 2048 -> 32768, Cubic W4 g128 from
+    N(0, 0.02), bf16 activations N(0, 1) at M = 2 (one sequence, one draft),
+    then the fused greedy acceptance of that sequence.  The lm_head is 37.9 MB,
+    so eight prepared copies rotate through each graph (303 MB, past the 256 MB
+    Infinity Cache); the step graph runs one lm_head copy and the acceptance."""
+    import torch
+
+    from cubic_serve_amd import linear, quantization as qz, sampling
+
+    n, k = 32768, 2048
+    g = torch.Generator(device=dev).manual_seed(10)
+    w = torch.randn((n, k), generator=g, device=dev) * 0.02
+    first = linear.prepare_matrix(qz.quantize_cubic(w, bits=4, group_in=GROUP), dev)
+    del w
+    copies = [first] + [linear.clone_prepared(first) for _ in range(7)]
+    x = torch.randn((2, k), generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.empty((2, n), dtype=torch.bfloat16, device=dev)
+    binds = [linear.bind_prepared(x, c, (logits,)) for c in copies]
+    lm_ms = time_graph(capture(lambda: [b.launch() for b in binds]), 10, 3) / len(binds)
+    torch.cuda.synchronize()
+    draft = logits[0].float().argmax().view(1, 1)  # a hit: the draft is the target argmax
+    q_scores = torch.full((1, 1, 20), float("nan"), dtype=torch.bfloat16, device=dev)
+    q_scores[:, :, 0] = 1.0
+    q_ids = torch.full((1, 1, 20), -1, dtype=torch.int64, device=dev)
+    q_ids[:, :, 0] = draft
+    zeros = torch.zeros((1, 1), dtype=torch.float32, device=dev)
+    plan = sampling.MTPVerifyPlan(
+        logits=logits, q_scores=q_scores, q_token_ids=q_ids, draft_tokens=draft.contiguous(),
+        temperatures=zeros, top_ps=torch.ones_like(zeros),
+        top_ks=torch.full((1, 1), 20, dtype=torch.int64, device=dev),
+        seeds=torch.zeros((1, 1), dtype=torch.int64, device=dev),
+        ordinals=torch.zeros((1, 1), dtype=torch.int64, device=dev))
+    acc_ms = time_graph(capture(lambda: [plan.launch() for _ in range(20)]), 10, 2) / 20
+    step = [0]
+
+    def one_step():
+        binds[step[0] % len(binds)].launch()
+        plan.launch()
+        step[0] += 1
+
+    step_ms = time_graph(capture(lambda: [one_step() for _ in range(len(binds))]), 10, 2) / len(binds)
+    merged = plan.merged.cpu().tolist()
+    return {"lm_head_us": round(lm_ms * 1e3, 2), "lm_head_gbs": round(gemm_bytes(2, n, k) / lm_ms / 1e6, 1),
+            "accept_us": round(acc_ms * 1e3, 2), "verify_step_us": round(step_ms * 1e3, 2),
+            "accepted": merged[0][0]}
 
 
 def measure_cfg5(dev) -> dict:
