@@ -195,13 +195,12 @@ def test_merge_prefix_matches_oracle(oracle):
 # --------------------------------------------------------------------------- #
 # fused verify from logits
 # --------------------------------------------------------------------------- #
-def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, live=None):
+def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, live=None, k=20):
     rng = np.random.default_rng(seed)
     g = torch.Generator().manual_seed(seed)
     rows = c * (depth + 1)
     target = (torch.randn((rows, width), generator=g) * 3).to(torch.bfloat16)
     tbits = to_bits(target)
-    k = 20
     temps = np.full((depth, c), 0.7 if stochastic else 0.0, np.float32)
     if stochastic:
         noise = (target.float().reshape(c, depth + 1, width)[:, :depth]
@@ -211,7 +210,7 @@ def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, li
         q_scores = qs.reshape(depth, c, k)
         q_ids = qid.reshape(depth, c, k)
         # drafts: q's first or second candidate (positive draft probability)
-        pick = (rng.random((depth, c)) < 0.2).astype(np.int64)
+        pick = ((rng.random((depth, c)) < 0.2) & (k > 1)).astype(np.int64)
         drafts = np.take_along_axis(q_ids, pick[..., None], -1)[..., 0]
     else:
         f = oracle.bf16_bits_to_f32(tbits)
@@ -224,7 +223,7 @@ def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, li
         q_scores[:, :, 0] = bf16([1.0])[0]
         q_ids[:, :, 0] = drafts
     top_ps = np.full((depth, c), 0.9 if stochastic else 1.0, np.float32)
-    top_ks = np.full((depth, c), 20, np.int64)
+    top_ks = np.full((depth, c), 20 if k == 20 else max(1, k - 2), np.int64)
     seeds = rng.integers(0, 2**40, (depth, c)).astype(np.int64)
     ordinals = rng.integers(0, 10000, (depth, c)).astype(np.int64)
     uniforms = rng.random((depth, c, 2)).astype(np.float32) if use_uniforms else None
@@ -236,7 +235,7 @@ def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, li
         seeds=torch.from_numpy(seeds).to(DEV), ordinals=torch.from_numpy(ordinals).to(DEV),
         uniforms=None if uniforms is None else torch.from_numpy(uniforms).to(DEV))
     want = oracle.verify_from_logits(tbits, q_scores, q_ids, drafts, temps, top_ps, top_ks, seeds,
-                                     ordinals, live, uniforms)
+                                     ordinals, live, uniforms, count=k)
     for _ in range(2):
         plan.launch(live_rows=live)
         torch.cuda.synchronize()
@@ -271,6 +270,13 @@ def test_fused_stochastic_cfg3_shape(oracle):
 def test_fused_small_shapes_and_dead_rows(oracle, use_uniforms):
     _fused_case(oracle, 5, 2, 3000, True, 11, use_uniforms=use_uniforms, live=3)
     _fused_case(oracle, 1, 1, 32768, False, 12)
+
+
+@pytest.mark.parametrize("k", [1, 3, 7, 16])
+@pytest.mark.parametrize("stochastic", [True, False])
+def test_fused_fewer_candidates(oracle, k, stochastic):
+    """Capacity below 20 (verification blocks of 1 to 16 lanes), top_k = k - 2."""
+    _fused_case(oracle, 6, 2, 9000, stochastic, 30 + k, k=k)
 
 
 @pytest.mark.parametrize("stochastic", [True, False])
