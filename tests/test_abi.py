@@ -94,3 +94,17 @@ def test_moe_router_and_compaction_arguments():
         _native.call("cubic_moe_compact", 16, 8, 0, 4, 0, 16, 16, 16, 16, 16, None)
     with pytest.raises(ValueError, match="experts"):
         _native.call("cubic_moe_compact", 16, 8, 0, 1025, 16, 16, 16, 16, 16, 16, None)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message (no GPU touched)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    res = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr
+    assert res.stdout == ""
