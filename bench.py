@@ -54,7 +54,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations (cfg3 W3 lm_head + stochastic "
                          "acceptance, cfg4 routed experts)")
-    ap.add_argument("--cpu-rows", type=int, default=6144,
+    ap.add_argument("--cpu-rows", type=int, default=18432,
                     help="lm_head rows in the CPU-baseline sample")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
                                                       "profiles", "gemm_lm_head_cfg2_traffic.md"),
