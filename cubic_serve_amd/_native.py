@@ -25,6 +25,9 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_prepare_weight": (I32, [I32, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P, I64,
                                    P, P, P]),
     "cubic_gemm_workspace_bytes": (I64, [I64, I64, I64, I32]),
+    "cubic_gemm_group_workspace_bytes": (I64, [I64, I32, I64, I64, I32]),
+    "cubic_gemm_grouped_workspace_bytes": (I64, [I64, I64, I64, I64, I32]),
+    "cubic_gemm_group": (I32, [P, I64, P, P, I64, I32, I64, I64, I32, I32, P, P, P, I64, P]),
     "cubic_gemm": (I32, [P, I64, P, P, I64, I64, I64, I32, I32, P, I64, P, I64, P]),
     "cubic_gemm_grouped": (I32, [P, I64, P, P, I64, I64, I64, I64, I32, I32, P, I64, P, I64, P,
                                  I64, P]),

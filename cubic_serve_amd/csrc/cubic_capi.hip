@@ -39,60 +39,67 @@ int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // ---------------------------------------------------------------------------
-// GEMM launch plan: a pure function of (n, k) so every output row sees the
-// same K partition and column grouping whatever m is.
+// GEMM launch plan.
+//
+// The K partition (split, blocks_per_split) is a pure function of ONE
+// member's (n, k): neither m nor the number of grouped members changes which
+// k-blocks a partition holds, so every output element is summed in the same
+// order whatever m is and whether or not its matrix shares a launch
+// (quantization/extensions/cubic/marlin.py:347-360 plans grouped launches on
+// one member for this reason; quantization/common/marlin/cost.py:59-79 keeps
+// partitions independent of m).  Tiles per wave (J) and the row chunking only
+// choose which wave computes a tile; they never change its arithmetic, so they
+// may follow the launch's total width and m.
 // ---------------------------------------------------------------------------
 struct GemmPlan {
     int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
     int chunk_rows;  // rows per grid-z chunk (64, or 32 when M is split across workgroups)
 };
 
-GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
+// K partition of one member: split in powers of two (at most 8) until a
+// partition holds at most 16 k-blocks and about 256 workgroups of one tile
+// per wave are in flight; a member wide enough to fill the GPU with two tiles
+// per wave keeps K whole.
+void plan_k(int64_t n_member, int64_t k, int* split_out, int* bps_out) {
+    const int64_t tiles = ceil_div(n_member, 16);
+    const int k_blocks = (int)ceil_div(k, kKBlock);
+    int split = 1;
+    if (ceil_div(tiles, 2 * cubic::kGemmWaves) < 256) {
+        const int64_t out_blocks = ceil_div(tiles, cubic::kGemmWaves);
+        while (split < 8 && (ceil_div(k_blocks, split) > 16 || out_blocks * split < 256)) split *= 2;
+        if (split > k_blocks / 2) split = k_blocks / 2 > 0 ? k_blocks / 2 : 1;
+    }
+    const int bps = (int)ceil_div(k_blocks, split);
+    *bps_out = bps;
+    *split_out = (int)ceil_div(k_blocks, bps);
+}
+
+GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k) {
     GemmPlan p;
+    const int64_t n = n_member * members;
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
+    plan_k(n_member, k, &p.split, &p.blocks_per_split);
     const int64_t chunks = ceil_div(m, 64);
-    int split = 1;
-    if (ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) * chunks >= 256) {
-        // Wide outputs (lm_head): two 16-column tiles per wave (half the
-        // activation bytes and A-fragment LDS reads per weight byte) and
-        // enough column blocks to fill the GPU without a K split, which also
-        // admits the three-workgroups-per-CU register cap.
-        p.tiles_per_wave = 2;
-    } else {
-        // Narrower outputs: one tile per wave, K split until a partition has
-        // at most 16 k-blocks and about 256 workgroups are in flight (measured
-        // best on the cfg2 layer shapes: qkv / o split 4, down split 8, gate/up
-        // split 2).
-        p.tiles_per_wave = 1;
-        const int64_t out_blocks = ceil_div(p.n_tiles, cubic::kGemmWaves) * chunks;
-        while (split < 8 && (ceil_div(p.k_blocks, split) > 16 || out_blocks * split < 256)) split *= 2;
-        if (split > p.k_blocks / 2) split = p.k_blocks / 2 > 0 ? p.k_blocks / 2 : 1;
-    }
-#if defined(CUBIC_TIMELINE) || defined(CUBIC_DEV_PLAN)  // instrumented builds only: plan overrides for sweeps
-    if (const char* e = getenv("CUBIC_DEV_J")) p.tiles_per_wave = atoi(e);
-    if (const char* e = getenv("CUBIC_DEV_SPLIT")) split = atoi(e);
-#endif
+    // Two 16-column tiles per wave (half the activation bytes and A-fragment
+    // LDS reads per weight byte) when K is whole and the launch still fills the
+    // GPU; one tile per wave otherwise.
+    p.tiles_per_wave = (p.split == 1 && ceil_div(p.n_tiles, 2 * cubic::kGemmWaves) * chunks >= 256) ? 2 : 1;
     p.col_blocks = (int)ceil_div(p.n_tiles, cubic::kGemmWaves * p.tiles_per_wave);
     // Rows 33..64 split over two 32-row workgroups when the grid would
     // otherwise hold fewer than two workgroups per CU (qkv, o: measured 7%
-    // faster; the weights are read twice, from L2 the second time).  Per-row
-    // arithmetic is unchanged, so results stay bitwise independent of M.
+    // faster; the weights are read twice, from L2 the second time).
     p.chunk_rows = 64;
-    if (p.tiles_per_wave == 1 && m > 32 && m <= 64 && (int64_t)p.col_blocks * split < 512)
+    if (p.tiles_per_wave == 1 && m > 32 && m <= 64 && (int64_t)p.col_blocks * p.split < 512)
         p.chunk_rows = 32;
-#if defined(CUBIC_TIMELINE) || defined(CUBIC_DEV_PLAN)
-    if (const char* e = getenv("CUBIC_DEV_MSPLIT")) p.chunk_rows = atoi(e) && m > 32 && m <= 64 ? 32 : 64;
-#endif
-    p.blocks_per_split = (int)ceil_div(p.k_blocks, split);
-    p.split = (int)ceil_div(p.k_blocks, p.blocks_per_split);
     return p;
 }
 
-// Split-K partials: per K partition and output block (64-row chunk x column
-// block), kGemmWaves waves x J tiles x MT m-tiles x 64 lanes float4 units.
-int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
-    const GemmPlan p = plan_gemm(m, n, k);
+// Split-K workspace: arrival counters per output block, then FP32 partials
+// per K partition and output block (64-row chunk x column block): kGemmWaves
+// waves x J tiles x MT m-tiles x 64 lanes float4 units.
+int64_t gemm_workspace(int64_t m, int64_t n_member, int members, int64_t k) {
+    const GemmPlan p = plan_gemm(m, n_member, members, k);
     if (p.split == 1) return 0;
     const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, p.chunk_rows);
     const int64_t mt = p.chunk_rows == 32 ? 2 : (ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1)));
@@ -101,36 +108,42 @@ int64_t gemm_workspace(int64_t m, int64_t n, int64_t k) {
 }
 
 int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-                int64_t m, int64_t n, int64_t n_split, int64_t k, int bits, int group_in,
-                void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
-                int64_t workspace_bytes, void* stream) {
-    if (!x || !codes || !meta || !y0) return fail(CUBIC_EINVAL, "null operand");
-    if (m <= 0 || n <= 0 || k <= 0 || m > (1 << 30) || n > (1 << 30) || k > (1 << 30))
+                int64_t m, int members, int64_t n_member, int64_t k, int bits, int group_in,
+                void* const* ys, const int64_t* ldys, void* workspace, int64_t workspace_bytes,
+                void* stream) {
+    if (!x || !codes || !meta || !ys) return fail(CUBIC_EINVAL, "null operand");
+    if (members < 1 || members > cubic::kMaxGemmMembers)
+        return fail(CUBIC_EINVAL, "members=%d outside 1..%d", members, cubic::kMaxGemmMembers);
+    for (int i = 0; i < members; ++i)
+        if (!ys[i]) return fail(CUBIC_EINVAL, "null output of member %d", i);
+    if (m <= 0 || n_member <= 0 || k <= 0 || m > (1 << 30) || n_member * members > (1 << 30) || k > (1 << 30))
         return fail(CUBIC_EINVAL, "gemm extents must be positive: m=%lld n=%lld k=%lld",
-                    (long long)m, (long long)n, (long long)k);
+                    (long long)m, (long long)n_member, (long long)k);
+    if (members > 1 && n_member % 16)
+        return fail(CUBIC_EINVAL, "grouped members need n %% 16 == 0 (n=%lld)", (long long)n_member);
     if (bits < 1 || bits > 8) return fail(CUBIC_ENOTSUP, "bits=%d outside 1..8", bits);
     if (group_in <= 0 || group_in % 32) return fail(CUBIC_ENOTSUP, "group_in=%d must be a multiple of 32", group_in);
     if (k % 8 || ldx % 8 || ldx < k || !aligned16(x))
         return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
-    if (ldy0 < (n_split) || (y1 && ldy1 < n - n_split))
-        return fail(CUBIC_EINVAL, "output leading dimension too small");
-    const GemmPlan p = plan_gemm(m, n, k);
-    const int64_t need = gemm_workspace(m, n, k);
+    for (int i = 0; i < members; ++i)
+        if (ldys[i] < n_member) return fail(CUBIC_EINVAL, "output leading dimension too small");
+    const GemmPlan p = plan_gemm(m, n_member, members, k);
+    const int64_t need = gemm_workspace(m, n_member, members, k);
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
     if (need && !workspace) return fail(CUBIC_EINVAL, "null workspace");
     cubic::GemmArgs a = {};
     a.x = (const uint16_t*)x;
     a.codes = codes;
     a.meta = meta;
-    a.y0 = (uint16_t*)y0;
-    a.y1 = (uint16_t*)y1;
+    for (int i = 0; i < members; ++i) {
+        a.ys[i] = (uint16_t*)ys[i];
+        a.ldys[i] = ldys[i];
+    }
     a.ldx = ldx;
-    a.ldy0 = ldy0;
-    a.ldy1 = ldy1;
     a.m = (int)m;
-    a.n = (int)n;
+    a.n = (int)(n_member * members);
     a.k = (int)k;
-    a.n_split = (int)n_split;
+    a.n_member = (int)n_member;
     a.bits = bits;
     a.group_in = group_in;
     a.k_blocks = p.k_blocks;
@@ -146,6 +159,12 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
         a.partials = (float*)((char*)workspace + counters);
     }
     return hip_status(cubic::launch_gemm(a, (hipStream_t)stream), "cubic_gemm launch");
+}
+
+// words of the prepared code stream / metadata of `tiles` 16-column tiles
+int64_t prepared_code_words(int64_t tiles, int64_t k, int bits) { return tiles * ceil_div(k, kKBlock) * 64 * bits; }
+int64_t prepared_meta_words(int64_t tiles, int64_t k, int bits, int group_in) {
+    return tiles * ceil_div(k, group_in) * 16 * (bits == 4 ? 4 : 2);
 }
 
 // ---------------------------------------------------------------------------
@@ -254,23 +273,63 @@ int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void
 
 int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits) {
     if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
-    return gemm_workspace(m, n, k);
+    return gemm_workspace(m, n, 1, k);
+}
+
+int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64_t n, int64_t k, int bits) {
+    if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8 || members < 1 ||
+        members > cubic::kMaxGemmMembers)
+        return -1;
+    return gemm_workspace(m, n, members, k);
+}
+
+int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, int64_t k, int bits) {
+    if (m <= 0 || n0 <= 0 || n1 <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
+    if (n0 == n1) return gemm_workspace(m, n0, 2, k);
+    const int64_t w0 = gemm_workspace(m, n0, 1, k), w1 = gemm_workspace(m, n1, 1, k);
+    return w0 > w1 ? w0 : w1;
 }
 
 int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
                int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
                void* workspace, int64_t workspace_bytes, void* stream) {
-    return gemm_common(x, ldx, codes, meta, m, n, n, k, bits, group_in, y, ldy, nullptr, 0,
-                       workspace, workspace_bytes, stream);
+    void* ys[1] = {y};
+    const int64_t ldys[1] = {ldy};
+    return gemm_common(x, ldx, codes, meta, m, 1, n, k, bits, group_in, ys, ldys, workspace,
+                       workspace_bytes, stream);
+}
+
+int cubic_gemm_group(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
+                     int64_t m, int members, int64_t n, int64_t k, int bits, int group_in,
+                     void* const* ys, const int64_t* ldys, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
+    if (!ys || !ldys) return fail(CUBIC_EINVAL, "null output table");
+    return gemm_common(x, ldx, codes, meta, m, members, n, k, bits, group_in, ys, ldys, workspace,
+                       workspace_bytes, stream);
 }
 
 int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
                        int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
                        void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
                        int64_t workspace_bytes, void* stream) {
-    if (!y1 || n0 <= 0 || n1 <= 0) return fail(CUBIC_EINVAL, "grouped gemm needs two members");
-    return gemm_common(x, ldx, codes, meta, m, n0 + n1, n0, k, bits, group_in, y0, ldy0, y1,
-                       ldy1, workspace, workspace_bytes, stream);
+    if (!y0 || !y1 || n0 <= 0 || n1 <= 0) return fail(CUBIC_EINVAL, "grouped gemm needs two members");
+    if (n0 % 16) return fail(CUBIC_EINVAL, "grouped gemm needs n0 %% 16 == 0 (n0=%lld)", (long long)n0);
+    if (n0 == n1) {
+        void* ys[2] = {y0, y1};
+        const int64_t ldys[2] = {ldy0, ldy1};
+        return gemm_common(x, ldx, codes, meta, m, 2, n0, k, bits, group_in, ys, ldys, workspace,
+                           workspace_bytes, stream);
+    }
+    // members of different widths have different K plans: one launch each, in
+    // stream order, sharing the workspace (every launch leaves it zero)
+    if (bits < 1 || bits > 8 || group_in <= 0 || group_in % 32 || k <= 0)
+        return fail(CUBIC_ENOTSUP, "invalid grouped geometry");
+    const int64_t off_c = prepared_code_words(n0 / 16, k, bits), off_m = prepared_meta_words(n0 / 16, k, bits, group_in);
+    const int rc = cubic_gemm(x, ldx, codes, meta, m, n0, k, bits, group_in, y0, ldy0, workspace,
+                              workspace_bytes, stream);
+    if (rc != CUBIC_OK) return rc;
+    return cubic_gemm(x, ldx, codes + off_c, meta + off_m, m, n1, k, bits, group_in, y1, ldy1,
+                      workspace, workspace_bytes, stream);
 }
 
 int cubic_moe_route(const void* logits, int logits_fp16, const int32_t* row_activity,
@@ -409,20 +468,19 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
     cubic_prepared_words(n, k, bits, group_in, &cw, &mw);
     if (expert_code_words < cw || expert_meta_words < mw)
         return fail(CUBIC_EINVAL, "expert strides smaller than one prepared matrix");
-    // no K split (routed launches have max_blocks x column blocks
-    // workgroups); two tiles per wave once there are >= 128 column blocks
-    const GemmPlan p = plan_gemm(64, n, k);
+    // no K split: routed launches have max_blocks x column blocks workgroups
+    const GemmPlan p = plan_gemm(64, n, 1, k);
     cubic::GemmArgs a = {};
     a.x = (const uint16_t*)x;
     a.codes = codes;
     a.meta = meta;
-    a.y0 = (uint16_t*)y;
+    a.ys[0] = (uint16_t*)y;
     a.ldx = ldx;
-    a.ldy0 = ldy;
+    a.ldys[0] = ldy;
     a.m = (int)(max_blocks * block_m);
     a.n = (int)n;
     a.k = (int)k;
-    a.n_split = (int)n;
+    a.n_member = (int)n;
     a.bits = bits;
     a.group_in = group_in;
     a.k_blocks = p.k_blocks;

@@ -13,6 +13,9 @@ namespace cubic {
 // workgroups measured slower on every cfg2 shape.
 constexpr int kGemmWaves = 4;
 
+// Members of one grouped GEMM launch (same K, same per-member width).
+constexpr int kMaxGemmMembers = 8;
+
 struct AcceptArgs {
     const uint16_t* logits;       // [rows, row_stride] bf16
     int64_t row_stride;           // elements
@@ -108,12 +111,14 @@ struct GemmArgs {
     const uint16_t* x;            // [m, k] bf16, row stride ldx
     const uint32_t* codes;        // prepared code tiles
     const uint32_t* meta;         // prepared (scale, a|b) per (column, group)
-    uint16_t* y0;                 // columns [0, n_split)
-    uint16_t* y1;                 // columns [n_split, n) or null
+    // member outputs: column n belongs to member n / n_member and lands at
+    // column n % n_member of ys[member] (row stride ldys[member])
+    uint16_t* ys[kMaxGemmMembers];
     float* partials;              // split-K FP32 partials or null
     uint32_t* counters;           // split-K arrival counters or null
-    int64_t ldx, ldy0, ldy1;
-    int m, n, k, n_split;
+    int64_t ldx;
+    int64_t ldys[kMaxGemmMembers];
+    int m, n, k, n_member;
     int bits, group_in;
     int k_blocks, groups_k;       // ceil(k / 128), ceil(k / group_in)
     int split, blocks_per_split;  // K partitions and k-blocks per partition

@@ -251,8 +251,9 @@ __device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buff
             const int umt = (u / kWave) % MT, ul = u % kWave;
             const int n = ((blockIdx.x * kGemmWaves + uw) * J + uj) * 16 + (ul & 15);
             if (n >= a.n) continue;
-            uint16_t* y = n < a.n_split ? a.y0 + n : a.y1 + (n - a.n_split);
-            const int64_t ldy = n < a.n_split ? a.ldy0 : a.ldy1;
+            const int member = n / a.n_member;
+            uint16_t* y = a.ys[member] + (n - member * a.n_member);
+            const int64_t ldy = a.ldys[member];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + umt * 16 + 4 * (ul >> 4) + r;
@@ -514,8 +515,9 @@ void gemm_kernel(GemmArgs a) {
         for (int j = 0; j < J; ++j) {
             const int n = (tile0 + j) * 16 + col;
             if (n >= a.n) continue;
-            uint16_t* y = n < a.n_split ? a.y0 + n : a.y1 + (n - a.n_split);
-            const int64_t ldy = n < a.n_split ? a.ldy0 : a.ldy1;
+            const int member = n / a.n_member;
+            uint16_t* y = a.ys[member] + (n - member * a.n_member);
+            const int64_t ldy = a.ldys[member];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll

@@ -31,6 +31,9 @@ from . import _native
 from .quantization import METADATA_IDS, QuantizedMatrix, partition_rows
 
 
+MAX_GROUP_MEMBERS = 8  # kMaxGemmMembers of the C ABI
+
+
 @dataclass(frozen=True, slots=True)
 class CubicLinearParameters:
     """Format parameters (quantization/extensions/cubic/policy.py:18-40 analogue).
@@ -103,8 +106,21 @@ def _storage(t: Tensor) -> int:
     return t.untyped_storage().data_ptr()
 
 
+def gemm_workspace_bytes(m: int, widths: Sequence[int], k: int, bits: int) -> int:
+    """Split-K workspace of one bound launch over members of the given widths."""
+    lib = _native.lib()
+    widths = tuple(widths)
+    if len(widths) == 1:
+        return lib.cubic_gemm_workspace_bytes(m, widths[0], k, bits)
+    if len(set(widths)) == 1:
+        return lib.cubic_gemm_group_workspace_bytes(m, len(widths), widths[0], k, bits)
+    if len(widths) == 2:
+        return lib.cubic_gemm_grouped_workspace_bytes(m, widths[0], widths[1], k, bits)
+    raise ValueError("grouped members of different widths are limited to two")
+
+
 class _GemmLaunch:
-    """One bound cubic_gemm / cubic_gemm_grouped call (immutable operands)."""
+    """One bound cubic_gemm / cubic_gemm_group / cubic_gemm_grouped call."""
 
     def __init__(self, x: Tensor, prepared: PreparedCubic, outputs: Sequence[Tensor],
                  widths: Sequence[int], workspace: Tensor | None):
@@ -112,6 +128,10 @@ class _GemmLaunch:
         self.workspace = workspace
         self.identity = tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype)
                               for t in (x, *self.outputs))
+        members = len(self.outputs)
+        # host tables of a same-width group, built once and kept alive here
+        self._ys = (_native.ctypes.c_void_p * members)(*(y.data_ptr() for y in self.outputs))
+        self._ldys = (_native.ctypes.c_int64 * members)(*(y.stride(0) for y in self.outputs))
 
     def validate(self) -> None:
         now = tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype)
@@ -129,6 +149,10 @@ class _GemmLaunch:
             _native.call("cubic_gemm", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
                          pr.meta.data_ptr(), m, pr.n, pr.k, pr.bits, pr.group_in, y.data_ptr(),
                          y.stride(0), ws_ptr, ws_bytes, stream)
+        elif len(set(self.widths)) == 1:
+            _native.call("cubic_gemm_group", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
+                         pr.meta.data_ptr(), m, len(self.widths), self.widths[0], pr.k, pr.bits,
+                         pr.group_in, self._ys, self._ldys, ws_ptr, ws_bytes, stream)
         else:
             y0, y1 = self.outputs
             _native.call("cubic_gemm_grouped", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
@@ -179,12 +203,14 @@ def arguments(operators: "PackedLinearOperators", matrix: QuantizedMatrix):
     p, e = matrix.payload, matrix.encoding
     dummy = next(iter(p.values()))
     key = id(matrix)
-    if key not in operators._partitions:
+    cached = operators._partitions.get(key)
+    if cached is None or cached[0] is not matrix:
+        # the matrix is kept in the value, so its id cannot be reused while cached
         counts = matrix.partitions or (matrix.shape[0],)
-        operators._partitions[key] = torch.tensor(
+        cached = operators._partitions[key] = (matrix, torch.tensor(
             [i for i, count in enumerate(counts) for _ in range(count // e.group_out)],
-            dtype=torch.int32, device=dummy.device)
-    parts = operators._partitions[key]
+            dtype=torch.int32, device=dummy.device))
+    parts = cached[1]
     if e.metadata == "int8-scale-int4-ab-global-fp32":
         return (p["weight_packed"], p["weight_scale"], dummy, p["weight_ab"], dummy,
                 p["weight_scale_global"], p["weight_a_global"], p["weight_b_global"], parts), 1
@@ -222,10 +248,16 @@ def bind_linear(operators, x, weight, output, params=None, fp8_token_scales=None
 
 
 def bind_grouped(operators, x, weights, outputs, params=None):
-    """Same-input members in one launch (:297-305); None if not admitted."""
-    if len(weights) != 2 or any(not admitted(w, x) for w in weights):
+    """Same-input members in one launch (:297-305); None if not admitted.
+
+    Members must share shape and encoding (cubic/marlin.py:347-360 plans the
+    launch on one member, so grouping never changes a member's K partition);
+    anything else is declined and bound as separate launches.
+    """
+    if not 2 <= len(weights) <= MAX_GROUP_MEMBERS or any(not admitted(w, x) for w in weights):
         return None
-    if weights[0].encoding != weights[1].encoding or weights[0].shape[0] % 16:
+    base = weights[0]
+    if any(w.encoding != base.encoding or w.shape != base.shape for w in weights) or base.shape[0] % 16:
         return None
     return operators._bind_gemm(x, tuple(weights), tuple(outputs))
 
@@ -326,12 +358,12 @@ class PackedLinearOperators:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("Cubic linears must be bound before graph capture")
         prepared = self.prepared(weights, x.device)
-        m, n = x.shape[0], prepared.n
-        ws_bytes = _native.lib().cubic_gemm_workspace_bytes(m, n, prepared.k, prepared.bits)
+        widths = [w.shape[0] for w in weights]
+        ws_bytes = gemm_workspace_bytes(x.shape[0], widths, prepared.k, prepared.bits)
         if ws_bytes < 0:
             raise ValueError("invalid GEMM geometry")
         workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
-        launch = _GemmLaunch(x, prepared, outputs, [w.shape[0] for w in weights], workspace)
+        launch = _GemmLaunch(x, prepared, outputs, widths, workspace)
         out = outputs[0] if len(outputs) == 1 else tuple(outputs)
         return PackedOperatorBinding(out, (launch,),
                                      scratch=(workspace,) if workspace is not None else ())
@@ -406,8 +438,9 @@ def bind_prepared(x: Tensor, prepared: PreparedCubic, outputs: Sequence[Tensor],
             raise ValueError("bound linear output has an invalid ABI")
     if x.dtype is not torch.bfloat16 or x.ndim != 2 or x.shape[1] != prepared.k:
         raise ValueError("bound linear requires bf16 [M, K] activations")
-    ws_bytes = _native.lib().cubic_gemm_workspace_bytes(x.shape[0], prepared.n, prepared.k,
-                                                        prepared.bits)
+    ws_bytes = gemm_workspace_bytes(x.shape[0], widths, prepared.k, prepared.bits)
+    if ws_bytes < 0:
+        raise ValueError("invalid GEMM geometry")
     workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
     launch = _GemmLaunch(x, prepared, outputs, widths, workspace)
     out = outputs[0] if len(outputs) == 1 else outputs

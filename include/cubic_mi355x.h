@@ -72,20 +72,42 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  * quantization/extensions/cubic/marlin.py:377-521 (bind_planned_linear :339)
  * and the small-row kernel of quantization/common/small_rows.cu:94-241.
  *
+ * K plan: the K partition of every output column is a function of its
+ * member's (n, k) only -- never of m, nor of how many members share a launch
+ * (quantization/extensions/cubic/marlin.py:347-360, common/marlin/cost.py:
+ * 59-79) -- so a row's result is bitwise the same for every m and grouped
+ * members equal separate launches bit for bit.
+ *
  * cubic_gemm_workspace_bytes: workspace for (m, n, k); 0 when no K split.
  *   The workspace must be zero-filled before its first use; every launch
  *   leaves it zero again.  One workspace per concurrently running launch.
  * cubic_gemm: single output y[m, ldy] (columns n).
- * cubic_gemm_grouped: two members sharing x (gate/up), prepared as one
- *   [n0 + n1, k] matrix; columns < n0 go to y0, the rest to y1
- *   (bind_linear_group, ops/cuda/linear/quantized.py:445-507;
- *   cubic/marlin.py:347 bind_planned_grouped).
+ * cubic_gemm_group: `members` (1..8) matrices of the same [n, k] shape and
+ *   encoding sharing x, prepared as one [members * n, k] matrix (member i's
+ *   prepared codes/metadata follow member i-1's); member i's columns go to
+ *   ys[i] (row stride ldys[i]); n % 16 == 0 when members > 1.  ys and ldys
+ *   are host arrays.  Replaces bind_planned_grouped (cubic/marlin.py:
+ *   347-360) behind bind_linear_group (ops/cuda/linear/quantized.py:445-507).
+ *   Workspace: cubic_gemm_group_workspace_bytes(m, members, n, k, bits).
+ * cubic_gemm_grouped: two members (gate/up), prepared as one [n0 + n1, k]
+ *   matrix; columns < n0 go to y0, the rest to y1; n0 % 16 == 0.  Equal
+ *   widths run as one cubic_gemm_group launch; unequal widths run as two
+ *   launches (each member keeps its own K plan).  Workspace:
+ *   cubic_gemm_grouped_workspace_bytes(m, n0, n1, k, bits).
  * x: bf16 [m, ldx], 16-byte aligned, ldx % 8 == 0.
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits);
+CUBIC_API int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64_t n, int64_t k,
+                                                   int bits);
+CUBIC_API int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, int64_t k,
+                                                     int bits);
 CUBIC_API int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
                int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
                void* workspace, int64_t workspace_bytes, void* stream);
+CUBIC_API int cubic_gemm_group(const void* x, int64_t ldx, const uint32_t* codes,
+                               const uint32_t* meta, int64_t m, int members, int64_t n, int64_t k,
+                               int bits, int group_in, void* const* ys, const int64_t* ldys,
+                               void* workspace, int64_t workspace_bytes, void* stream);
 CUBIC_API int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
                        int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
                        void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,

@@ -153,16 +153,15 @@ def test_split_k_path_enclosure_and_repeatability(oracle):
 
 
 def test_row_is_invariant_to_m_and_permutation():
-    # Up to 64 rows (one row chunk: the verify regime) the launch plan, and so
-    # each row's summation order, does not depend on M; beyond that the K split
-    # shrinks with M, so invariance is checked under permutation at fixed M.
+    # The launch plan's K partition depends on (n, k) only, so each row's
+    # summation order is the same for every M, also past one 64-row chunk.
     n, k = 4096, 4096
     m = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(1)) * 0.02, 4)
     md = m.to(DEV)
     ops = linear.PackedLinearOperators()
     base = torch.randn((130, k), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
     ref = ops.linear(base[:1].contiguous(), md)
-    for mrows in (3, 8, 17, 33, 64):
+    for mrows in (3, 8, 17, 33, 64, 65, 130):
         y = ops.linear(base[:mrows].contiguous(), md)
         assert torch.equal(y[:1], ref), mrows
     for mrows in (64, 65, 130):
