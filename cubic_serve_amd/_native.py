@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_accept_workspace_bytes": (I64, [I32, I32, I32]),
     "cubic_accept": (I32, [P, I64, I32, I32, I32, I32, P, P, P, I32, P, P, P, P, P, P, P, P, P, P,
                            P, P, P, I64, P]),
+    "cubic_accept_noalloc": (I32, [P, I64, I32, I32, I32, I32, P, P, P, I32, P, P, P, P, P, P, P, P,
+                                   P, P, P, P, P]),
 }
 
 

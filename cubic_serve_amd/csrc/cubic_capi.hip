@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstdarg>
 #include <cstdlib>
+#include <mutex>
 
 #include "cubic_mi355x.h"
 #include "cubic_capi_internal.h"
@@ -216,6 +217,56 @@ int next_pow2(int v) {
     while (p < v) p <<= 1;
     return p;
 }
+
+// ---------------------------------------------------------------------------
+// Static acceptance scratch for cubic_accept_noalloc: arrival counters, tile
+// survivor keys and flags, in device memory that the library owns for the life
+// of the process (one copy per device).  The name below is a host-side handle;
+// device code only ever sees the address hipGetSymbolAddress returns for the
+// current device.  Launches leave the counters zero, as cubic_accept does; the
+// array starts zero (zero-initialised device global) and set-up clears it once
+// per device with a fill kernel.
+// ---------------------------------------------------------------------------
+constexpr int64_t kAcceptScratchBytes = int64_t(4) << 20;
+__device__ __align__(256) uint32_t scratch[kAcceptScratchBytes / 4];
+
+__global__ void clear_words_kernel(uint32_t* p, int64_t words) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Address of the current device's scratch; set up on the first call per device.
+int accept_scratch(hipStream_t stream, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(CUBIC_ENOTSUP, "device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        clear_words_kernel<<<256, 256, 0, stream>>>((uint32_t*)ptr, kAcceptScratchBytes / 4);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_status(e, "scratch clear launch");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return CUBIC_OK;
+}
+
+int accept_common(const void* logits, int64_t row_stride, int width, int c, int depth,
+                  int live_rows, const float* row_temperatures, const void* q_scores,
+                  const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
+                  const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                  const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
+                  void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
+                  int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream);
 
 }  // namespace
 
@@ -634,6 +685,46 @@ int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int d
                  const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
                  void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
                  int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!workspace) return fail(CUBIC_EINVAL, "null operand");
+    return accept_common(logits, row_stride, width, c, depth, live_rows, row_temperatures, q_scores,
+                         q_ids, capacity, draft_tokens, temperatures, top_ps, top_ks, seeds, ordinals,
+                         uniforms, cand_scores, cand_ids, decisions, merged, emitted, workspace,
+                         workspace_bytes, stream);
+}
+
+int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int c, int depth,
+                         int live_rows, const float* row_temperatures, const void* q_scores,
+                         const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
+                         const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                         const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
+                         void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
+                         int64_t* emitted, void* stream) {
+    if (c >= 1 && depth >= 1 && depth <= 8) {
+        const int64_t need = accept_workspace(c * (depth + 1), c, width);
+        if (need > kAcceptScratchBytes)
+            return fail(CUBIC_EWORKSPACE, "accept scratch needs %lld bytes; the static scratch holds %lld",
+                        (long long)need, (long long)kAcceptScratchBytes);
+    }
+    void* scratch_ptr = nullptr;
+    const int rc = accept_scratch((hipStream_t)stream, &scratch_ptr);
+    if (rc != CUBIC_OK) return rc;
+    return accept_common(logits, row_stride, width, c, depth, live_rows, row_temperatures, q_scores,
+                         q_ids, capacity, draft_tokens, temperatures, top_ps, top_ks, seeds, ordinals,
+                         uniforms, cand_scores, cand_ids, decisions, merged, emitted, scratch_ptr,
+                         kAcceptScratchBytes, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int accept_common(const void* logits, int64_t row_stride, int width, int c, int depth,
+                  int live_rows, const float* row_temperatures, const void* q_scores,
+                  const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
+                  const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                  const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
+                  void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
+                  int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream) {
     if (!logits || !row_temperatures || !q_scores || !q_ids || !draft_tokens || !temperatures ||
         !top_ps || !top_ks || !seeds || !ordinals || !cand_scores || !cand_ids || !decisions ||
         !merged || !workspace)
@@ -682,4 +773,4 @@ int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int d
     return hip_status(cubic::launch_accept(a, true, (hipStream_t)stream), "cubic_accept launch");
 }
 
-}  // extern "C"
+}  // namespace

@@ -294,6 +294,29 @@ CUBIC_API int cubic_accept(const void* logits, int64_t row_stride, int width, in
                  void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
                  int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * cubic_accept_noalloc: cubic_accept with no workspace argument.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same operands, results and errors as cubic_accept.
+ * Its scratch is a 4 MiB static device array per GPU, held until the process
+ * ends; calls whose plan needs more (cubic_accept_workspace_bytes(c, depth,
+ * width) > 4 MiB) fail with CUBIC_EWORKSPACE.  The first call on a device
+ * resolves and clears that device's array.  Nothing here calls hipMalloc,
+ * hipFree or an allocating library routine.  Every call on one GPU shares the
+ * array and it keeps the last call's contents: calls that overlap on one GPU
+ * (launches on concurrent streams) race and must be ordered by the caller.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int c,
+                                   int depth, int live_rows, const float* row_temperatures,
+                                   const void* q_scores, const int64_t* q_ids, int capacity,
+                                   const int64_t* draft_tokens, const float* temperatures,
+                                   const float* top_ps, const int64_t* top_ks,
+                                   const int64_t* seeds, const int64_t* ordinals,
+                                   const float* uniforms, void* cand_scores, int64_t* cand_ids,
+                                   int64_t* decisions, int64_t* merged, int64_t* emitted,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif
