@@ -55,7 +55,14 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 struct GemmPlan {
     int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
     int chunk_rows;  // rows per grid-z chunk (64, or 32 when M is split across workgroups)
+    int rows_waves;  // > 0: small-row kernel, this many waves per tile, blocks_per_split per wave
 };
+
+// Small-row regime (the reference's small_rows path, M <= 4): one tile per
+// workgroup, K split over the workgroup's waves; a function of k alone.
+bool small_rows(int64_t m, int bits, int group_in) {
+    return m >= 1 && m <= 4 && bits <= 4 && group_in > 0 && group_in % kKBlock == 0;
+}
 
 // K partition of one member: split in powers of two (at most 8) until a
 // partition holds at most 16 k-blocks and about 256 workgroups of one tile
@@ -75,11 +82,21 @@ void plan_k(int64_t n_member, int64_t k, int* split_out, int* bps_out) {
     *split_out = (int)ceil_div(k_blocks, bps);
 }
 
-GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k) {
+GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits, int group_in) {
     GemmPlan p;
     const int64_t n = n_member * members;
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
+    p.rows_waves = 0;
+    if (small_rows(m, bits, group_in)) {
+        p.rows_waves = p.k_blocks > 32 ? 8 : 4;
+        p.blocks_per_split = (int)ceil_div(p.k_blocks, p.rows_waves);
+        p.split = 1;
+        p.tiles_per_wave = 1;
+        p.col_blocks = p.n_tiles;
+        p.chunk_rows = 4;
+        return p;
+    }
     plan_k(n_member, k, &p.split, &p.blocks_per_split);
     const int64_t chunks = ceil_div(m, 64);
     // Two 16-column tiles per wave (half the activation bytes and A-fragment
@@ -99,8 +116,8 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k) {
 // Split-K workspace: arrival counters per output block, then FP32 partials
 // per K partition and output block (64-row chunk x column block): kGemmWaves
 // waves x J tiles x MT m-tiles x 64 lanes float4 units.
-int64_t gemm_workspace(int64_t m, int64_t n_member, int members, int64_t k) {
-    const GemmPlan p = plan_gemm(m, n_member, members, k);
+int64_t gemm_workspace(int64_t m, int64_t n_member, int members, int64_t k, int bits, int group_in) {
+    const GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
     if (p.split == 1) return 0;
     const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, p.chunk_rows);
     const int64_t mt = p.chunk_rows == 32 ? 2 : (ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1)));
@@ -128,8 +145,8 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
         return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
     for (int i = 0; i < members; ++i)
         if (ldys[i] < n_member) return fail(CUBIC_EINVAL, "output leading dimension too small");
-    const GemmPlan p = plan_gemm(m, n_member, members, k);
-    const int64_t need = gemm_workspace(m, n_member, members, k);
+    const GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
+    const int64_t need = gemm_workspace(m, n_member, members, k, bits, group_in);
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
     if (need && !workspace) return fail(CUBIC_EINVAL, "null workspace");
     cubic::GemmArgs a = {};
@@ -154,6 +171,7 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
     a.n_tiles = p.n_tiles;
     a.tiles_per_wave = p.tiles_per_wave;
     a.chunk_rows = p.chunk_rows;
+    a.rows_waves = p.rows_waves;
     if (p.split > 1) {
         const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, p.chunk_rows) * 4);  // one per output block
         a.counters = (uint32_t*)workspace;
@@ -324,20 +342,20 @@ int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void
 
 int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits) {
     if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
-    return gemm_workspace(m, n, 1, k);
+    return gemm_workspace(m, n, 1, k, bits, -1);  // group unknown: the MFMA plan bounds both
 }
 
 int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64_t n, int64_t k, int bits) {
     if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8 || members < 1 ||
         members > cubic::kMaxGemmMembers)
         return -1;
-    return gemm_workspace(m, n, members, k);
+    return gemm_workspace(m, n, members, k, bits, -1);
 }
 
 int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, int64_t k, int bits) {
     if (m <= 0 || n0 <= 0 || n1 <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
-    if (n0 == n1) return gemm_workspace(m, n0, 2, k);
-    const int64_t w0 = gemm_workspace(m, n0, 1, k), w1 = gemm_workspace(m, n1, 1, k);
+    if (n0 == n1) return gemm_workspace(m, n0, 2, k, bits, -1);
+    const int64_t w0 = gemm_workspace(m, n0, 1, k, bits, -1), w1 = gemm_workspace(m, n1, 1, k, bits, -1);
     return w0 > w1 ? w0 : w1;
 }
 
@@ -520,7 +538,7 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
     if (expert_code_words < cw || expert_meta_words < mw)
         return fail(CUBIC_EINVAL, "expert strides smaller than one prepared matrix");
     // no K split: routed launches have max_blocks x column blocks workgroups
-    const GemmPlan p = plan_gemm(64, n, 1, k);
+    const GemmPlan p = plan_gemm(64, n, 1, k, bits, group_in);
     cubic::GemmArgs a = {};
     a.x = (const uint16_t*)x;
     a.codes = codes;

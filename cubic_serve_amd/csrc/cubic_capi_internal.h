@@ -125,6 +125,8 @@ struct GemmArgs {
     int n_tiles;                  // ceil(n / 16)
     int tiles_per_wave;           // J: 16-column tiles per wave (1, 2, 4)
     int chunk_rows;               // rows per grid-z chunk: 64, or 32 (M split), or block_m (routed)
+    int rows_waves;               // > 0: small-row kernel with this many waves per tile
+                                  // (blocks_per_split = k-blocks per wave)
     // routed experts (MoE, routed != 0): workgroup chunk z covers the
     // 16 * MT padded route slots [z * 16 * MT, ...) of one expert
     // (block_expert[z]); a slot holds a route ordinal, or `routes` for

@@ -562,6 +562,140 @@ void gemm_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Small-row GEMM (M <= 4; bits <= 4; groups of whole k-blocks)
+//   grid.x: 16-column tiles; a workgroup of G waves owns one tile and all of K.
+//   Wave w streams the tile's k-blocks [w * kbw, (w + 1) * kbw) in chunks of
+//   D: codes, the group's level table and the activation fragments of every
+//   row (rows past M re-read row M-1; their outputs are never stored), all
+//   loaded straight into registers -- no LDS staging and no barrier in the
+//   loop.  The MFMA sums each 32-k fragment; the G per-wave
+//   partial sums are added in wave order through LDS at the end, so the K
+//   partition depends on K alone (not on M or on grouping).
+// (quantization/common/small_rows.cu:94-241 and small_rows_cost.py:438-501
+// are the reference's small-row path: a separate arithmetic for M <= 4.)
+// ---------------------------------------------------------------------------
+template <int BITS, int G, int D>
+__global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
+    constexpr int W = BITS;
+    constexpr int MW = meta_words<BITS>();
+    constexpr int kOut = 0x7FFFFFF0;  // buffer offset past every range: the load returns 0, no fetch
+    __shared__ float red[G][16][4];
+    // wave index as a scalar: the per-wave K range and loop bounds stay uniform
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int q = lane >> 4, col = lane & 15;
+    const int tile = blockIdx.x;
+    const int kb_begin = wave * a.blocks_per_split;
+    const int kb_end = min(kb_begin + a.blocks_per_split, a.k_blocks);
+    const int nkb = kb_end - kb_begin;  // may be <= 0 for trailing waves
+    // Buffer views of this tile's codes and metadata and of the activations.
+    // Out-of-range offsets read zero without touching memory: rows at or past
+    // M, quarters past K, and k-blocks past the wave's range (the tail of its
+    // last chunk) all come back as zero codes / zero activations, so they add
+    // exactly 0 to the accumulator with no masking instructions.
+    const __amdgpu_buffer_rsrc_t codes = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(a.codes + (int64_t)tile * a.k_blocks * kWave * W), 0,
+        a.k_blocks * kWave * W * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t meta = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(a.meta + (int64_t)tile * a.groups_k * 16 * MW), 0, a.groups_k * 16 * MW * 4,
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.x), 0, (int)((int64_t)a.m * a.ldx * 2), 0x00020000);
+    const int gpk = a.group_in / kKBlock;  // k-blocks per metadata group
+    const int x_lane = col < a.m ? (int)((int64_t)col * a.ldx * 2) + 64 * q : kOut;
+
+    uint32_t rc[D][W];
+    uint32_t rm[D][MW];
+    u32x4_dev_t ra[D][4];
+    auto load = [&](int i, uint32_t (&c)[W], uint32_t (&mm)[MW], u32x4_dev_t (&av)[4]) {
+        const int kb = kb_begin + i;
+        const bool live = i < nkb;
+        const int co = live ? (kb * kWave + lane) * W * 4 : kOut;
+        if constexpr (W == 4) {
+            const u32x4_dev_t v = __builtin_amdgcn_raw_buffer_load_b128(codes, co, 0, 2);  // nt
+            c[0] = v.x; c[1] = v.y; c[2] = v.z; c[3] = v.w;
+        } else if constexpr (W == 2) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(codes, co, 0, 2);
+            c[0] = v[0]; c[1] = v[1];
+        } else if constexpr (W == 3) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b96(codes, co, 0, 2);
+            c[0] = v[0]; c[1] = v[1]; c[2] = v[2];
+        } else {
+            c[0] = __builtin_amdgcn_raw_buffer_load_b32(codes, co, 0, 2);
+        }
+        const int mo = live ? ((kb / gpk) * 16 + col) * MW * 4 : kOut;
+        if constexpr (MW == 4) {
+            const u32x4_dev_t v = __builtin_amdgcn_raw_buffer_load_b128(meta, mo, 0, 0);
+            mm[0] = v.x; mm[1] = v.y; mm[2] = v.z; mm[3] = v.w;
+        } else {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(meta, mo, 0, 0);
+            mm[0] = v[0]; mm[1] = v[1];
+        }
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int k0 = kb * kKBlock + 32 * q + 8 * f;
+            const int xo = live && k0 < a.k ? x_lane + (kb * kKBlock + 8 * f) * 2 : kOut;
+            av[f] = __builtin_bit_cast(u32x4_dev_t, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
+        }
+    };
+    floatx4_t acc = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    // Chunks of D k-blocks: every load of a chunk is issued before its first
+    // use and none is carried across the loop edge (a load still in flight at
+    // the back-edge makes the compiler drain the counter at the loop head);
+    // the other waves of the CU cover each chunk's latency.
+    for (int i0 = 0; i0 < nkb; i0 += D) {
+#pragma unroll
+        for (int st = 0; st < D; ++st) load(i0 + st, rc[st], rm[st], ra[st]);
+#pragma unroll
+        for (int st = 0; st < D; ++st) {
+            LevelTable tab;
+            tab.lo_lo = rm[st][0];
+            tab.hi_lo = rm[st][1];
+            tab.lo_hi = MW == 4 ? rm[st][MW == 4 ? 2 : 0] : 0u;
+            tab.hi_hi = MW == 4 ? rm[st][MW == 4 ? 3 : 1] : 0u;
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                const uint4 bw = decode_fragment<BITS>(rc[st], f, tab);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ra[st][f]),
+                                                              __builtin_bit_cast(bf16x8_t, bw), acc, 0, 0, 0);
+            }
+        }
+    }
+    // rows 0..3 of the tile are lanes 0..15 (quarter 0), one register per row
+    if (q == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][col][r] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0 && q == 0) {
+        const int n = tile * 16 + col;
+        if (n < a.n) {
+            float sum[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[r] = red[0][col][r];
+#pragma unroll
+            for (int w = 1; w < G; ++w)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sum[r] += red[w][col][r];
+            const int member = n / a.n_member;
+            uint16_t* y = a.ys[member] + (n - member * a.n_member);
+            const int64_t ldy = a.ldys[member];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (r < a.m) y[(int64_t)r * ldy] = (uint16_t)float_to_bf16_bits(sum[r]);
+        }
+    }
+}
+
+template <int BITS>
+hipError_t launch_rows_bits(const GemmArgs& a, int g, hipStream_t s) {
+    dim3 grid(a.n_tiles);
+    if (g == 8) rows_kernel<BITS, 8, 4><<<grid, 8 * 64, 0, s>>>(a);
+    else rows_kernel<BITS, 4, 4><<<grid, 4 * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Load-time preparation
 // ---------------------------------------------------------------------------
 // Metadata: per (column, group) words; padding columns are zero.  bits <= 4:
@@ -767,6 +901,15 @@ hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t 
 // host plan: J from n, the K split from the number of output blocks (so a
 // row's result is the same for every m up to one 64-row chunk).
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+    if (a.rows_waves > 0) {  // small-row plan (host: M <= 4, bits <= 4, whole-k-block groups)
+        switch (a.bits) {
+            case 1: return launch_rows_bits<1>(a, a.rows_waves, s);
+            case 2: return launch_rows_bits<2>(a, a.rows_waves, s);
+            case 3: return launch_rows_bits<3>(a, a.rows_waves, s);
+            case 4: return launch_rows_bits<4>(a, a.rows_waves, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     // routed: one grid chunk per padded route block (a.m = block capacity)
     const int mt = a.routed ? a.block_m / 16 : (a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1));
     const int rows_chunks = (a.m + a.chunk_rows - 1) / a.chunk_rows;

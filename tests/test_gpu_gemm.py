@@ -154,16 +154,19 @@ def test_split_k_path_enclosure_and_repeatability(oracle):
 
 def test_row_is_invariant_to_m_and_permutation():
     # The launch plan's K partition depends on (n, k) only, so each row's
-    # summation order is the same for every M, also past one 64-row chunk.
+    # summation order is the same for every M of one arithmetic regime: the
+    # small-row kernel (M <= 4) and the MFMA-tile kernel (M >= 5), also past
+    # one 64-row chunk.
     n, k = 4096, 4096
     m = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(1)) * 0.02, 4)
     md = m.to(DEV)
     ops = linear.PackedLinearOperators()
     base = torch.randn((130, k), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
-    ref = ops.linear(base[:1].contiguous(), md)
-    for mrows in (3, 8, 17, 33, 64, 65, 130):
-        y = ops.linear(base[:mrows].contiguous(), md)
-        assert torch.equal(y[:1], ref), mrows
+    for regime in ((1, 2, 3, 4), (5, 8, 17, 33, 64, 65, 130)):
+        ref = ops.linear(base[:regime[0]].contiguous(), md)[:1]
+        for mrows in regime[1:]:
+            y = ops.linear(base[:mrows].contiguous(), md)
+            assert torch.equal(y[:1], ref), mrows
     for mrows in (64, 65, 130):
         perm = torch.randperm(mrows, generator=torch.Generator().manual_seed(3)).to(DEV)
         y = ops.linear(base[:mrows].contiguous(), md)
@@ -220,9 +223,13 @@ def test_wide_output_repeatable_and_row_invariant(oracle):
     for start in (0, 512 * 128 - 128, 600 * 128, n - 256):
         part = m.rows(start, start + 256).to("cpu")
         _check_linear(oracle, part, x, first[:, start:start + 256])
-    for mrows in (1, 2, 17, 33):
+    for mrows in (5, 17, 33):
         y = ops.linear(x[:mrows].contiguous(), m)
         assert torch.equal(y, first[:mrows]), mrows
+    small = ops.linear(x[:4].contiguous(), m)  # the small-row regime (M <= 4)
+    for mrows in (1, 2):
+        y = ops.linear(x[:mrows].contiguous(), m)
+        assert torch.equal(y, small[:mrows]), mrows
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
@@ -232,7 +239,7 @@ def test_llama70b_cfg5_shapes_sampled_enclosure(oracle, bits):
     28672 -> 8192), weights N(0, 0.02), at M = 1, 8, 64, 512: every sampled
     output inside the FP64 enclosure (64 columns per linear at a position that
     moves with M; at M = 512 the first and last 64-row chunks), and a row's
-    output equal for M = 1, 8 and 64 (one 64-row chunk)."""
+    output equal for M = 8 and 64 (MFMA-tile regime)."""
     print(f"cfg5 bits={bits}", flush=True)
     hidden, qkv, inter = 8192, 10240, 28672
     g = torch.Generator(device=DEV).manual_seed(100 + bits)
@@ -266,5 +273,5 @@ def test_llama70b_cfg5_shapes_sampled_enclosure(oracle, bits):
         if mrows == 64:
             for name, m in mats.items():
                 xin = xd if name == "down" else x
-                for sub in (1, 8):
+                for sub in (8,):
                     assert torch.equal(ops.linear(xin[:sub].contiguous(), m), outs[name][:sub]), (name, sub)
