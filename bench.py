@@ -12,8 +12,9 @@ own copy of the prepared weights (distinct HBM), so nothing is served from the
 graph and replayed; inputs are resident in HBM before the timed region.
 
 Prints one JSON line: value = algorithmic bytes of the step / step time
-(GB/s); roofline for the dominant kernel (the lm_head GEMM); cpu_baseline =
-the CPU oracle on a bounded sample of the same step.
+(GB/s); per-kernel launch times and HBM fractions; roofline for the kernel
+with the largest share of the step; cpu_baseline = the reference's eager torch
+path restated on the host cores, on a bounded sample of the same step.
 """
 from __future__ import annotations
 
@@ -54,13 +55,14 @@ def parse_args(argv=None):
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary configurations (cfg3 W3 lm_head + stochastic "
                          "acceptance, cfg4 routed experts)")
-    ap.add_argument("--cpu-rows", type=int, default=18432,
+    ap.add_argument("--cpu-rows", type=int, default=32768,
                     help="lm_head rows in the CPU-baseline sample")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                                      "profiles", "gemm_lm_head_cfg2_traffic.md"),
-                    help="measured HBM bytes per lm_head launch (line 'hbm_bytes_per_launch: N')")
-    ap.add_argument("--kernel-only", action="store_true",
-                    help="profiling aid: launch only the lm_head GEMM, eagerly, --steps times")
+                                                      "profiles", "gemm_layers_cfg2_counters.md"),
+                    help="measured HBM bytes per launch (lines 'hbm_bytes_per_launch[<kernel>]: N')")
+    ap.add_argument("--kernel-only", default=None, choices=("lm_head", "qkv", "o", "gate_up", "down"),
+                    help="profiling aid: launch only this GEMM (every layer's copy for the layer "
+                         "linears), eagerly, --steps times")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="profiling aid: run --steps elementwise negations over this many bytes "
                          "(reads and writes each byte once; scales the HBM traffic counters)")
@@ -96,6 +98,7 @@ def build_step(layers: int):
 
     layer_bindings = []
     gate_up = None
+    last = None
     for layer in range(layers):
         w = {k: (v if layer == 0 else linear.clone_prepared(v)) for k, v in proto.items()}
         gate_up = linear.PreparedCubic(torch.cat([w["gate"].codes, w["up"].codes]),
@@ -107,6 +110,7 @@ def build_step(layers: int):
             linear.bind_prepared(x, gate_up, (y_gate, y_up), (INTER, INTER)),
             linear.bind_prepared(x_down, w["down"], (y_down,)),
         ]
+        last = dict(qkv=w["qkv"], o=w["o"], gate_up=gate_up, down=w["down"])
         del w
     del proto
     lm_binding = linear.bind_prepared(x, lm_head, (logits,))
@@ -131,8 +135,53 @@ def build_step(layers: int):
         top_ks=torch.full((DEPTH, C_SEQ), 20, dtype=torch.int64, device=dev),
         seeds=torch.zeros((DEPTH, C_SEQ), dtype=torch.int64, device=dev),
         ordinals=torch.zeros((DEPTH, C_SEQ), dtype=torch.int64, device=dev))
+    outputs = dict(qkv=(y_qkv,), o=(y_o,), gate_up=(y_gate, y_up), down=(y_down,))
     return dict(layer_bindings=layer_bindings, lm_binding=lm_binding, plan=plan, logits=logits,
-                x=x, lm_head=lm_head, drafts=drafts, hit=hit)
+                x=x, x_down=x_down, lm_head=lm_head, drafts=drafts, hit=hit, last=last,
+                outputs=outputs)
+
+
+LINEARS = ("qkv", "o", "gate_up", "down")
+
+
+def linear_shapes() -> dict:
+    return {"qkv": (QKV, HIDDEN), "o": (HIDDEN, HIDDEN), "gate_up": (2 * INTER, HIDDEN),
+            "down": (HIDDEN, INTER)}
+
+
+def check_last_layer(step: dict) -> dict:
+    """After the timed replays: the graph's outputs of the last layer (every
+    layer writes the same buffers) equal a fresh eager launch of that layer's
+    weights into separate buffers, bit for bit."""
+    import torch
+
+    from cubic_serve_amd import linear
+
+    result = {}
+    for name in LINEARS:
+        graph_out = step["outputs"][name]
+        fresh = tuple(torch.empty_like(y) for y in graph_out)
+        xin = step["x_down"] if name == "down" else step["x"]
+        widths = (INTER, INTER) if name == "gate_up" else None
+        linear.bind_prepared(xin, step["last"][name], fresh, widths).launch()
+        torch.cuda.synchronize()
+        same = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(graph_out, fresh))
+        if not same:
+            raise AssertionError(f"{name}: graph-replayed output differs from an eager launch")
+        result[name] = "bitwise equal"
+    return result
+
+
+def time_linears(step: dict, layers: int) -> dict:
+    """Average launch time of each layer linear: the launches of all layers of
+    one kind, captured back to back in one graph (distinct weights per layer),
+    replayed with HIP events on the replay stream."""
+    per = {}
+    for i, name in enumerate(LINEARS):
+        binds = step["layer_bindings"][i::4]
+        ms = time_graph(capture(lambda: [b.launch() for b in binds]), 10, 2)
+        per[name] = ms / len(binds)
+    return per
 
 
 def capture(fn):
@@ -186,33 +235,44 @@ def time_eager(fn, reps: int, warmup: int) -> float:
 
 
 def cpu_baseline(step: dict, rows: int) -> dict:
-    """CPU oracle (scalar C, 1 thread) on a bounded sample of the same step:
-    decode + bf16 round + FP32 dot for lm_head rows [0, rows) at M = 64, and
-    the candidate preparation of all 64 logit rows."""
-    import numpy as np
+    """The reference's eager WNA16 path restated in torch on the host cores
+    (oracle/torch_ref.py: decode_matrix + one FP32 matmul per input row), on a
+    bounded sample of the step: lm_head rows [0, rows) at M = 64 (random
+    W4 g128 fmt0 payload of that shape), plus the greedy argmax of all 64
+    logit rows.  Median of 5 runs; ``cores`` = torch threads used."""
+    import statistics
+
     import torch
 
-    from oracle import oracle
-    from cubic_serve_amd import quantization as qz
+    from oracle import torch_ref
 
-    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    w = torch.randn((rows, HIDDEN), generator=g) * 0.02
-    m = qz.quantize_cubic(w, bits=BITS, group_in=GROUP)
-    payload = {k: v.numpy() for k, v in m.payload.items()}
-    x = step["x"].cpu().view(torch.int16).numpy().view(np.uint16)
-    logits = step["logits"].cpu().view(torch.int16).numpy().view(np.uint16)
-    t0 = time.perf_counter()
-    wb = oracle.decode_bf16(payload, BITS, qz.FMT_F32, (rows, HIDDEN), GROUP)
-    oracle.linear_bf16(x, wb)
-    t1 = time.perf_counter()
-    oracle.candidates(logits, np.zeros(M_ROWS, np.float32), 20)
-    t2 = time.perf_counter()
+    groups = (rows, HIDDEN // GROUP)
+    packed = torch.randint(0, 256, (rows, HIDDEN * BITS // 8), generator=g, dtype=torch.int32).to(torch.uint8)
+    scale = torch.rand(groups, generator=g) * 0.05
+    a = (torch.rand(groups, generator=g) * 1.5 - 0.25).half()
+    b = (torch.rand(groups, generator=g) - 0.5).half()
+    x = step["x"].cpu()
+    logits = step["logits"].cpu()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        w = torch_ref.decode_fmt0(packed, scale, a, b, BITS, GROUP, HIDDEN)
+        torch_ref.linear_rows(x, w)
+        logits.float().argmax(dim=-1)
+        times.append(time.perf_counter() - t0)
+        del w
+    med = statistics.median(times)
     nbytes = gemm_bytes(M_ROWS, rows, HIDDEN) + M_ROWS * VOCAB * 2
-    return {"value": round(nbytes / (t2 - t0) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/cubic_oracle.c: lm_head rows [0,{rows}) x K=4096 W4 at M=64 "
-                      f"(decode, bf16 round, FP32 dot: {t1 - t0:.2f}s) + candidates over "
-                      f"[64,151936] logits ({t2 - t1:.2f}s); same algorithmic-byte accounting"}
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle/torch_ref.py (torch {torch.__version__}, {torch.get_num_threads()} threads): "
+                      f"decode_matrix + per-row FP32 linear for lm_head rows [0,{rows}) x K=4096 W4 g128 "
+                      f"at M=64, plus greedy argmax over [64,151936] logits; median of 5 runs "
+                      f"{med:.2f}s (runs {', '.join(f'{t:.2f}' for t in times)}); same algorithmic-byte "
+                      f"accounting as the GPU value"}
 
 
 def measure_extras() -> dict:
@@ -523,8 +583,11 @@ def main(argv=None) -> int:
         return 0
     step = build_step(args.layers)
     if args.kernel_only:
+        binds = ([step["lm_binding"]] if args.kernel_only == "lm_head"
+                 else step["layer_bindings"][LINEARS.index(args.kernel_only)::4])
         for _ in range(args.steps):
-            step["lm_binding"].launch()
+            for b in binds:
+                b.launch()
         torch.cuda.synchronize()
         return 0
 
@@ -554,20 +617,36 @@ def main(argv=None) -> int:
     wall = time.perf_counter() - wall0
     ms_per_step = start.elapsed_time(end) / args.steps
 
-    # component breakdown and the dominant kernel's launch duration
-    lm_ms = time_eager(step["lm_binding"].launch, 50, 5)
+    layer_check = check_last_layer(step)
+
+    # component breakdown: every linear's average launch, the lm_head and the
+    # fused acceptance (HIP events on the stream the launches run on)
+    per_ms = time_linears(step, args.layers)
+    per_ms["lm_head"] = time_graph(capture(step["lm_binding"].launch), 50, 5)
     acc_graph = capture(lambda: step["plan"].launch())
     acc_ms = time_graph(acc_graph, 200, 10)
 
     nb = step_bytes(args.layers)
     value = nb["total"] / (ms_per_step * 1e-3) / 1e9
-    lm_gbs = nb["lm_head"] / (lm_ms * 1e-3) / 1e9
-    traffic = None
+    shapes = linear_shapes()
+    kernels = {}
+    for name, ms in per_ms.items():
+        n, k = shapes.get(name, (VOCAB, HIDDEN))
+        launches = args.layers if name in shapes else 1
+        byts = gemm_bytes(M_ROWS, n, k)
+        gbs = byts / (ms * 1e-3) / 1e9
+        kernels[name] = {"us": round(ms * 1e3, 2), "bytes_per_launch": byts, "gbs": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "share_of_step": round(launches * ms / ms_per_step, 4)}
+    dominant = max(kernels, key=lambda k: kernels[k]["share_of_step"])
+    traffic = {}
     if os.path.exists(args.traffic):
         with open(args.traffic) as f:
             for line in f:
-                if line.startswith("hbm_bytes_per_launch:"):
-                    traffic = int(line.split(":", 1)[1])
+                if line.startswith("hbm_bytes_per_launch["):
+                    key, val = line.split(":", 1)
+                    traffic[key[len("hbm_bytes_per_launch["):-1]] = int(val)
+    dom = kernels[dominant]
     result = {
         "metric": "verify-step µs + Cubic-GEMM HBM GB/s (% peak), Qwen3-8B-shaped W4, M=64",
         "value": round(value, 2),
@@ -587,16 +666,18 @@ def main(argv=None) -> int:
                    "m": M_ROWS, "layers": args.layers, "bits": BITS, "group": GROUP},
         "verify_step_us": round(ms_per_step * 1e3, 2),
         "step_hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "lm_head_us": round(lm_ms * 1e3, 2),
+        "lm_head_us": kernels["lm_head"]["us"],
         "accept_us": round(acc_ms * 1e3, 2),
         "accept_gbs": round(nb["accept"] / (acc_ms * 1e-3) / 1e9, 2),
-        "layers_us": round((ms_per_step - lm_ms - acc_ms) * 1e3, 2),
+        "layers_us": round(sum(kernels[n]["us"] for n in LINEARS) * args.layers, 2),
         "greedy_accepted": f"{accepted}/{C_SEQ}",
+        "layer_check": layer_check,
         "wall_s": round(wall, 3),
-        "roofline": {"kernel": "gemm_kernel<4,4,2,true,true> (lm_head)", "bound": "hbm",
-                     "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": nb["lm_head"]},
+        "kernels": kernels,
+        "roofline": {"kernel": f"{dominant} GEMM (largest share of the step)", "bound": "hbm",
+                     "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["frac"], "traffic": traffic.get(dominant),
+                     "bytes_per_launch": dom["bytes_per_launch"]},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_rows)

@@ -12,6 +12,7 @@ import struct
 
 import numpy as np
 import pytest
+import torch
 
 FMT0, FMT1, FMT2 = (
     "float32-scale-float16-ab",
@@ -263,3 +264,41 @@ def test_bf16_and_half_conversions_match_numpy_and_torch(oracle):
         f = np.array([h], np.uint16).view(np.float16).astype(np.float32)[0]
         got_f = lib.oracle_half_to_float(h)
         assert (math.isnan(got_f) and math.isnan(f)) or got_f == f
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_torch_restatement_decode_equals_c_oracle(oracle, bits):
+    """The CPU baseline's torch decode (oracle/torch_ref.py) is bit-equal to the
+    C oracle for every code value, with groups of 64 and a K tail."""
+    from oracle import torch_ref
+
+    n, k, gi = 24, 200, 64
+    g = torch.Generator().manual_seed(bits)
+    row_bytes = (k * bits + 7) // 8
+    packed = torch.randint(0, 256, (n, row_bytes), generator=g, dtype=torch.int32).to(torch.uint8)
+    groups = (n, (k + gi - 1) // gi)
+    payload = {"weight_packed": packed, "weight_scale": torch.rand(groups, generator=g) * 0.05,
+               "weight_a": (torch.rand(groups, generator=g) * 1.5 - 0.25).half(),
+               "weight_b": (torch.rand(groups, generator=g) - 0.5).half()}
+    want = oracle.decode_bf16({key: v.numpy() for key, v in payload.items()}, bits,
+                              "float32-scale-float16-ab", (n, k), gi)
+    got = torch_ref.decode_fmt0(payload["weight_packed"], payload["weight_scale"], payload["weight_a"],
+                                payload["weight_b"], bits, gi, k)
+    got = got.view(torch.int16).numpy().view(np.uint16).copy()
+    got[got == 0x8000] = 0
+    want = want.copy()
+    want[want == 0x8000] = 0
+    assert np.array_equal(got, want)
+
+
+def test_torch_restatement_linear_within_one_bf16_step(oracle):
+    from oracle import torch_ref
+
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((5, 384), generator=g).to(torch.bfloat16)
+    w = (torch.randn((40, 384), generator=g) * 0.02).to(torch.bfloat16)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    wb = w.view(torch.int16).numpy().view(np.uint16)
+    _, want = oracle.linear_bf16(xb, wb)
+    got = torch_ref.linear_rows(x, w).float().numpy()
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 1e-6)
