@@ -105,22 +105,37 @@ def verify_one_draft_candidates(
             decisions.data_ptr(), _native.stream_of(q_scores.device))
 
 
-_TensorABI = tuple
+# Operands of one root-sampling launch, in argument order: name, accepted
+# dtypes, and whether the tensor is a candidate grid [TP, C, K] or a per-row
+# vector [C].
+_ROOT_OPERANDS = (
+    ("scores", (torch.bfloat16, torch.float16), "grid"),
+    ("token_ids", (torch.int64,), "grid"),
+    ("temperatures", (torch.float32,), "row"),
+    ("top_ps", (torch.float32,), "row"),
+    ("top_ks", (torch.int64,), "row"),
+    ("seeds", (torch.int64,), "row"),
+    ("ordinals", (torch.int64,), "row"),
+    ("output_tokens", (torch.int64,), "row"),
+    ("output_valid", (torch.bool,), "row"),
+)
+_MAX_TP, _MAX_K = 8, 20
 
 
-def _abi(tensor: Tensor) -> _TensorABI:
-    if not isinstance(tensor, Tensor):
+def _fingerprint(t: Tensor | None):
+    """What a captured launch depends on besides the data: geometry, dtype
+    and device (None for an absent optional operand)."""
+    if t is None:
+        return None
+    if not isinstance(t, Tensor):
         raise TypeError("sampling operands must be tensors")
-    return tuple(tensor.shape), tensor.stride(), tensor.dtype, tensor.device
-
-
-def _next_power_of_2(n: int) -> int:
-    return 1 << (n - 1).bit_length()
+    return (t.dtype, t.device, tuple(t.shape), t.stride())
 
 
 @dataclass(frozen=True, slots=True)
 class RootTopKTopPSamplingMeta:
-    """Complete fixed launch identity for gathered ``[TP,C,K]`` candidates."""
+    """Launch identity for gathered ``[TP, C, K]`` candidates; ``block`` is
+    the candidate count TP*K rounded up to a power of two."""
 
     device: torch.device
     tp: int
@@ -130,10 +145,13 @@ class RootTopKTopPSamplingMeta:
 
 
 class RootTopKTopPSamplingPrimitive:
-    """Sample root-owned TP candidates without allocations or host RNG state.
+    """Root-owned top-k/top-p sampling over TP-gathered candidates.
 
-    Same constructor, ``launch`` and validation as topk_topp.py:141-278; the
-    launch is cubic_root_sample (one wave per row).
+    The launch allocates nothing and keeps no host RNG state: each row draws
+    from (seed, ordinal).  The operands given to the constructor fix the
+    launch; ``launch`` accepts only tensors of the same geometry.  Interface
+    of ops/cuda/sampling/topk_topp.py:141-278; the kernel is
+    cubic_root_sample (one wave per row).
     """
 
     def __init__(self, scores: Tensor, token_ids: Tensor, temperatures: Tensor, top_ps: Tensor,
@@ -142,21 +160,21 @@ class RootTopKTopPSamplingPrimitive:
                  constrained_rows: Tensor | None = None) -> None:
         if type(allow_underfilled) is not bool:
             raise TypeError("candidate underfill policy must be boolean")
-        self.allow_underfilled = allow_underfilled
-        self._constraint_abi = None if constrained_rows is None else _abi(constrained_rows)
         operands = (scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals,
                     output_tokens, output_valid)
-        self._validate(operands)
-        if constrained_rows is not None and (
-                not allow_underfilled or constrained_rows.dtype != torch.bool
-                or constrained_rows.shape != temperatures.shape
-                or constrained_rows.device != temperatures.device
-                or not constrained_rows.is_contiguous()):
-            raise ValueError("invalid constrained-row ownership for root sampling")
+        self._check_operands(operands)
+        self._fixed_constraint = _fingerprint(constrained_rows)
+        if constrained_rows is not None:
+            usable = (allow_underfilled and constrained_rows.dtype == torch.bool
+                      and constrained_rows.shape == temperatures.shape
+                      and constrained_rows.device == temperatures.device
+                      and constrained_rows.is_contiguous())
+            if not usable:
+                raise ValueError("invalid constrained-row ownership for root sampling")
+        self.allow_underfilled = allow_underfilled
+        self._fixed = tuple(_fingerprint(t) for t in operands)
         tp, rows, k = scores.shape
-        self._abis = tuple(_abi(t) for t in operands)
-        self.meta = RootTopKTopPSamplingMeta(device=scores.device, tp=tp, rows=rows,
-                                             candidates_per_rank=k, block=_next_power_of_2(tp * k))
+        self.meta = RootTopKTopPSamplingMeta(scores.device, tp, rows, k, 1 << (tp * k - 1).bit_length())
 
     @property
     def launch_signature(self) -> str:
@@ -167,12 +185,12 @@ class RootTopKTopPSamplingPrimitive:
     def launch(self, scores: Tensor, token_ids: Tensor, temperatures: Tensor, top_ps: Tensor,
                top_ks: Tensor, seeds: Tensor, ordinals: Tensor, output_tokens: Tensor,
                output_valid: Tensor, *, constrained_rows: Tensor | None = None) -> None:
-        """Enqueue one fixed-shape launch on the current stream."""
+        """Enqueue one launch on the device's current stream."""
         operands = (scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals,
                     output_tokens, output_valid)
-        if tuple(_abi(t) for t in operands) != self._abis:
+        if tuple(_fingerprint(t) for t in operands) != self._fixed:
             raise ValueError("sampling operands do not match the fixed launch ABI")
-        if (None if constrained_rows is None else _abi(constrained_rows)) != self._constraint_abi:
+        if _fingerprint(constrained_rows) != self._fixed_constraint:
             raise ValueError("constrained-row ownership differs from the fixed launch ABI")
         m = self.meta
         with torch.cuda.device(m.device):
@@ -184,25 +202,21 @@ class RootTopKTopPSamplingPrimitive:
                          _native.stream_of(m.device))
 
     @staticmethod
-    def _validate(operands: tuple) -> None:
-        if any(not isinstance(t, Tensor) for t in operands):
-            raise TypeError("sampling operands must be tensors")
-        scores, token_ids, temperatures, top_ps, top_ks, seeds, ordinals, tokens, valid = operands
-        if any(t.device.type != "cuda" or not t.is_contiguous() for t in operands):
+    def _check_operands(operands: tuple) -> None:
+        for t in operands:
+            _fingerprint(t)
+        if not all(t.device.type == "cuda" and t.is_contiguous() for t in operands):
             raise ValueError("all sampling operands must be contiguous CUDA tensors")
-        if len({t.device for t in operands}) != 1:
+        if len({t.device for t in operands}) > 1:
             raise ValueError("all sampling operands must share one CUDA device")
-        if scores.ndim != 3 or not (1 <= scores.shape[0] <= 8) or not (1 <= scores.shape[2] <= 20):
+        grid = operands[0].shape
+        if len(grid) != 3 or not 1 <= grid[0] <= _MAX_TP or not 1 <= grid[2] <= _MAX_K:
             raise ValueError("scores must be FP16/BF16 [TP,C,K] with TP<=8 and K<=20")
-        row_shape = (scores.shape[1],)
-        if (scores.shape[1] <= 0
-                or scores.dtype not in (torch.bfloat16, torch.float16)
-                or token_ids.dtype is not torch.int64 or token_ids.shape != scores.shape
-                or temperatures.dtype is not torch.float32 or top_ps.dtype is not torch.float32
-                or top_ks.dtype is not torch.int64 or seeds.dtype is not torch.int64
-                or ordinals.dtype is not torch.int64 or tokens.dtype is not torch.int64
-                or valid.dtype is not torch.bool
-                or any(t.shape != row_shape for t in operands[2:])):
+        expected_shape = {"grid": grid, "row": (grid[1],)}
+        conforming = grid[1] > 0 and all(
+            t.dtype in dtypes and t.shape == expected_shape[role]
+            for t, (_, dtypes, role) in zip(operands, _ROOT_OPERANDS))
+        if not conforming:
             raise ValueError("expected FP16/BF16 scores/int64 ids [TP,C,K], FP32 temperature/top_p, "
                              "int64 top_k/seed/ordinal/token, and bool valid [C]")
 
