@@ -21,18 +21,6 @@
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
 
-#ifdef CUBIC_TIMELINE
-// Development instrumentation (never built into the shipped library).
-__device__ uint64_t g_acc_timeline[4096][24];
-extern "C" __attribute__((visibility("default"))) int cubic_dev_acc_timeline(uint64_t* host) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_acc_timeline), sizeof(g_acc_timeline));
-}
-#define ACC_STAMP(slot) \
-    do { if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 4096) \
-        g_acc_timeline[blockIdx.x + gridDim.x * blockIdx.y][(slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define ACC_STAMP(slot) do {} while (0)
-#endif
 
 namespace cubic {
 namespace {
@@ -436,19 +424,16 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         p1set.s[s] = p1s; p1set.i[s] = p1i; p1set.r[s] = v < block && p1r;
     }
     const bool pairs_valid = __all(lane_ok);
-    ACC_STAMP(16);
     LaneSet<SLOTS> q, p0, p1;
     const int qc = select_set<SLOTS>(qset, block, r.k, lane, sc, q);
     const int p0c = select_set<SLOTS>(p0set, block, r.k, lane, sc, p0);
     const int p1c = select_set<SLOTS>(p1set, block, r.k, lane, sc, p1);
 
-    ACC_STAMP(17);
     float qp[SLOTS], p0p[SLOTS], p1p[SLOTS], qm, p0m, p1m;
     probabilities<SLOTS>(q.s, r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
     probabilities<SLOTS>(p0.s, r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
     probabilities<SLOTS>(p1.s, r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
 
-    ACC_STAMP(18);
     float t1[SLOTS], t2[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
@@ -469,7 +454,6 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
     const bool greedy_accepted = r.draft == p0_top;
     const bool accepted = greedy ? greedy_accepted : random_accepted;
     wave_lds_sync();
-    ACC_STAMP(19);
 
     float q_at_p[SLOTS], residual[SLOTS];
 #pragma unroll
@@ -486,7 +470,6 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         residual[s] = d > 0.0f ? d : 0.0f;
         t1[s] = residual[s];
     }
-    ACC_STAMP(20);
     const float rmass = vl_tree_sum<SLOTS>(t1, block);
     const float u_sample = r.has_uniforms ? r.u1
                                       : philox_uniform(key ^ 0x85EBCA6Bu, (uint32_t)(r.ordinal * 2 + 1));
@@ -513,7 +496,6 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         if (p1_slot < block && p1_slot / kWave == s) p1_token = a1;
         if (res_slot < block && res_slot / kWave == s) res_token = ar;
     }
-    ACC_STAMP(21);
     const int64_t need = (greedy || r.underfilled) ? 1 : r.top_k;
     const bool valid = r.active && pairs_valid && r.rows_ok && r.temperature >= 0.0f &&
                        r.temperature < __builtin_huge_valf() && r.top_k >= 1 && r.top_k <= r.k &&
@@ -566,7 +548,6 @@ __device__ __forceinline__ uint32_t sortable_score(float f) {
 __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArgs a) {
     __shared__ RootScratch sc;
     const int row = blockIdx.x, v = threadIdx.x, w = v / kWave, lane = v % kWave;
-    ACC_STAMP(0);
     const int count = a.tp * a.k;
     const bool cm = v < count;
     float score = -__builtin_huge_valf();
@@ -594,7 +575,6 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
             sc.counts[w][2] = __builtin_popcountll(bw);
         }
     }
-    ACC_STAMP(1);
     __syncthreads();
     int malformed = 0, real_count = 0, wide_count = 0;
 #pragma unroll
@@ -623,7 +603,6 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
             rank += (int)(sc.real[j] & ahead);
         }
     }
-    ACC_STAMP(2);
     if (real) { sc.sorted_score[rank] = score; sc.sorted_id[rank] = id; }
     __syncthreads();
     // a sorted pair equal to its predecessor is a duplicate: it takes no slot
@@ -641,7 +620,6 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     if (in && !dup && distinct < a.k) { sc.sel_score[distinct] = ps; sc.sel_id[distinct] = pi; }
     __syncthreads();
     if (v >= kWave) return;
-    ACC_STAMP(3);
 
     const float temperature = a.temperatures[row], top_p = a.top_ps[row];
     const int64_t top_k = a.top_ks[row], seed = a.seeds[row], ordinal = a.ordinals[row];
@@ -657,12 +635,10 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     const int64_t sel_id = sc.sel_id[lane];
     float retained[1], mass;
     probabilities<1, false>(sorted, temperature, top_k, top_p, kWave, lane, retained, mass);
-    ACC_STAMP(4);
     const int64_t random_seed = seed ^ (seed >> 32) ^ (ordinal >> 32);
     const float uniform = philox_uniform2((uint32_t)random_seed, (uint32_t)((uint64_t)random_seed >> 32),
                                           (uint32_t)ordinal);
     const float target = uniform * mass;
-    ACC_STAMP(5);
     vl_scan<1>(retained, kWave, lane);
     const uint64_t hit = __ballot(retained[0] > target);
     const int sampled = hit ? __builtin_ctzll(hit) : kWave;
@@ -670,7 +646,6 @@ __global__ __launch_bounds__(kRootThreads) void root_sample_kernel(RootSampleArg
     const int64_t token = readlane64(sel_id, chosen & (kWave - 1));
     const bool valid = malformed == 0 && params_ok && enough &&
                        (greedy || (mass > 0.0f && sampled < kWave));
-    ACC_STAMP(6);
     if (lane == 0) {
         a.output_tokens[row] = valid ? token : -1;
         a.output_valid[row] = valid ? 1 : 0;
@@ -814,7 +789,6 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
             nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
             key2[e][w] = order_key16x2(word) & valid;
         }
-    ACC_STAMP(11);
     // 2. lane maxima (packed), then tau16 = the kTop-th largest lane maximum
     //    (ballot radix select): kTop lanes hold distinct elements of value
     //    >= tau16, so every element of the top kTop has a key >= tau16.
@@ -834,7 +808,6 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
         if (__popcll(__ballot(lane_max >= cand)) >= kTop) tau = cand;
     }
     const uint32_t thr = tau > 0u ? tau : 1u;  // empty elements never survive
-    ACC_STAMP(12);
     // 3. compact survivors (key >= thr) as composites.  Each lane marks the
     //    words holding a survivor (saturating packed subtract: nonzero iff a
     //    half is >= thr) and spills its keys to LDS word-major (lane-distinct
@@ -874,7 +847,6 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
         }
     }
     wave_lds_sync();  // the spill is rewritten by this wave's next tile only
-    ACC_STAMP(13);
     if (lane < kTop) out_top[lane] = 0u;
     if (total <= kWave) {
         // zero padding up to a multiple of 4 (slots past the survivors)
@@ -888,7 +860,6 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
             rank += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
         }
         wave_lds_sync();
-        ACC_STAMP(14);
         if (lane < (int)total && rank < (uint32_t)kTop) out_top[rank] = v;
     } else {
         // many equal values: kTop rounds of "largest composite below the previous"
@@ -963,7 +934,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     const int chunks = (width_left + kChunk - 1) / kChunk;
     const uint16_t* src = a.logits + (int64_t)row * a.row_stride + begin;
 
-    ACC_STAMP(0);
     uint4 raw[EMAX];
     const bool vec = a.vector_loads != 0;
     if (owned && vec && chunks * kChunk <= width_left) {
@@ -1000,7 +970,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     VerifyPrefetch pre = {};
     if (FUSED && wave < a.group_rows - 1) pre = prefetch_verify(a, (int64_t)wave * a.c + group, lane);
     const bool greedy_row = a.row_temperatures[row] == 0.0f;  // row-uniform
-    ACC_STAMP(1);
     // wave top-kTop of this wave's share (the maximum alone for a greedy
     // row), then the workgroup's top-kTop
     const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
@@ -1011,7 +980,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     const uint32_t bad = __any(nonfinite);
     if (lane == 0) ts.flags[wave] = bad;
     __syncthreads();
-    ACC_STAMP(2);
     uint32_t* part = a.partial_keys + ((int64_t)row * a.tiles + tile) * kTop;
     // workgroup top-kTop: every wave ranks its kTop entries among all
     // kWaves * kTop (nonzero composites are distinct; zeros are padding)
@@ -1035,9 +1003,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                          ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3]);
     }
     // arrival: the last workgroup of this row group finalises it
-    ACC_STAMP(3);
-    if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) { ACC_STAMP(4); return; }
-    ACC_STAMP(5);
+    if (!arrive_last(&a.counters[group], (uint32_t)(a.group_rows * a.tiles), &ts.last)) return;
 
     // ---- finalise the group's rows: merge tiles, publish candidates -------
     const int row0 = group * a.group_rows;
@@ -1062,7 +1028,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                     e = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
                 }
             }
-            if (gr == 0) ACC_STAMP(6);
             e = wave_max_u64(e);
             my = lane == 0 ? e : 0ull;
         } else {
@@ -1082,10 +1047,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                     }
                 }
             }
-            if (gr == 0) ACC_STAMP(6);
             my = wave_topk_u64<kPer>(entry, a.tiles * kTop, want, lane, ts.merge[wave]);
         }
-        if (gr == 0) ACC_STAMP(7);
         const int j = lane;  // capacity <= 64
         if (j < a.capacity) {
             uint16_t sc = 0x7FC0u;
@@ -1112,11 +1075,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     }
     if (!FUSED) {
         if (threadIdx.x == 0) store_device(&a.counters[group], 0u);
-        ACC_STAMP(8);
         return;
     }
     __syncthreads();
-    ACC_STAMP(8);
     // ---- fused: verify each depth of sequence `group`, merge the prefix ----
     const int c = group, depth = a.group_rows - 1;
     for (int d = wave; d < depth; d += kWaves) {
@@ -1174,7 +1135,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
     }
     __syncthreads();
-    ACC_STAMP(9);
     if (threadIdx.x == 0) {
         int64_t accepted = depth, bonus = ts.decisions[depth - 1][1];
         bool good = true;
@@ -1196,7 +1156,6 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
         store_device(&a.counters[group], 0u);
     }
-    ACC_STAMP(10);
 }
 
 template <int EMAX, bool FUSED>

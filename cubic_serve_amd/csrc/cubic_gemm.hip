@@ -24,19 +24,6 @@
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
 
-#ifdef CUBIC_TIMELINE
-// Development instrumentation (never built into the shipped library): per
-// workgroup s_memrealtime stamps of the GEMM main loop.
-__device__ uint64_t g_timeline[4096][40];
-extern "C" __attribute__((visibility("default"))) int cubic_dev_timeline(uint64_t* host) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), sizeof(g_timeline));
-}
-#define CUBIC_STAMP(slot) \
-    do { if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 4096 && (slot) < 40) \
-        g_timeline[blockIdx.x + gridDim.x * blockIdx.y][(slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define CUBIC_STAMP(slot) do {} while (0)
-#endif
 
 namespace cubic {
 namespace {
@@ -381,7 +368,6 @@ void gemm_kernel(GemmArgs a) {
             dst[i] = *reinterpret_cast<const uint4*>(act_row[i] + (kofs + act_c8 < a.k ? kofs : 0));
     };
 
-    CUBIC_STAMP(0);
 #pragma unroll
     for (int st = 0; st < S; ++st) load_codes(kb_begin + st, ring_codes[st], ring_meta[st]);
 #pragma unroll
@@ -418,7 +404,6 @@ void gemm_kernel(GemmArgs a) {
             // LDS hand-off only: no vector-memory drain at the barrier
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
-            CUBIC_STAMP(1 + kb - kb_begin);
             load_act(kb + NA, act[st % NA]);
             __builtin_amdgcn_sched_barrier(0);  // keep the prefetch where it is issued
 
@@ -509,7 +494,6 @@ void gemm_kernel(GemmArgs a) {
     }
 
     // --- epilogue -----------------------------------------------------------
-    CUBIC_STAMP(34);
     if (a.split == 1) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
@@ -545,9 +529,7 @@ void gemm_kernel(GemmArgs a) {
             store_device4(part, split * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
                           acc[mt][j]);
     __shared__ uint32_t last;
-    CUBIC_STAMP(35);
-    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) { CUBIC_STAMP(36); return; }
-    CUBIC_STAMP(37);
+    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
     switch (a.split) {
         case 2: reduce_partials<2, J, MT>(a, part, split_bytes, m0); break;
         case 3: reduce_partials<3, J, MT>(a, part, split_bytes, m0); break;
@@ -557,7 +539,6 @@ void gemm_kernel(GemmArgs a) {
         case 7: reduce_partials<7, J, MT>(a, part, split_bytes, m0); break;
         default: reduce_partials<8, J, MT>(a, part, split_bytes, m0); break;
     }
-    CUBIC_STAMP(38);
     if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
 }
 
@@ -868,9 +849,6 @@ __global__ void expand_metadata_kernel(int fmt, const void* m0, const void* m1, 
 
 template <int BITS, int MT, bool G128>
 hipError_t launch_g(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
-#ifdef CUBIC_TIMELINE
-    if (j == 4) { gemm_kernel<BITS, MT, 4, G128><<<grid, kGemmThreads, 0, s>>>(a); return hipGetLastError(); }
-#endif
     if constexpr (MT == 4 && BITS <= 5) {
         if (j == 2 && a.split == 1) {
             gemm_kernel<BITS, MT, 2, G128, true><<<grid, kGemmThreads, 0, s>>>(a);
