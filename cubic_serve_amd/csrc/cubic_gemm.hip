@@ -33,13 +33,14 @@ constexpr int kThreads = 256;                  // prepare / expand kernels
 constexpr int kGemmThreads = kGemmWaves * 64;  // gemm_kernel
 constexpr int kKBlock = 128;
 // Activation stage in LDS: per 16-row block, 16-byte chunk c (k = 8c..8c+7 of
-// the k-block) of row r sits in 16-byte slot c * 16 + (r ^ c).  An MFMA
-// A-fragment read (16 rows of one chunk per 16 lanes) and a row-contiguous
-// write (16 chunks of one row per 16 lanes) then each touch 16 distinct slots
-// of one 256-byte line: measured ~1.6x the read throughput of a padded
-// row-major tile on gfx950.
+// the k-block) of row r sits in 16-byte slot c * 16 + (r ^ (c & 3) << 2 ^ c >> 2).
+// An MFMA A-fragment read (lane (col, q) reads row col, chunk 4q + f) then
+// lands in position col ^ 4f ^ q of its 256-byte line, and the staging write
+// (lanes 0..15 store rows 0..15 of one chunk) in position r ^ g(c): both run at
+// the b128 peak rate of gfx950's LDS (measured 243 B/clk/CU for the reads,
+// 83 B/clk/CU for the writes; the plain r ^ c swizzle reads at 128).
 constexpr int kAStage = 64 * kKBlock;  // bf16 per stage (64 rows)
-__device__ __forceinline__ int a_slot(int r16, int c) { return c * 16 + (r16 ^ c); }
+__device__ __forceinline__ int a_slot(int r16, int c) { return c * 16 + (r16 ^ ((c & 3) << 2) ^ (c >> 2)); }
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float floatx4_t;
@@ -203,23 +204,58 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&dst)[
     }
 }
 
-// Code/metadata prefetch depth in k-blocks.  Two: deeper rings cost the
-// registers of a third resident workgroup per CU and measured slower on every
-// cfg2 shape.
-template <int BITS, int J>
-struct Stages {
-    static constexpr int value = 2;
-};
+
+// Output block staging: the block's bf16 results (16 * MT rows x C columns)
+// sit row-major in LDS with a row pitch of C + 8 elements (16-byte aligned
+// rows; the 2-byte writes of the four lane quarters land 16 banks apart).
+// store_tile then writes 16-byte row segments: eight consecutive columns of
+// one member, when the address is 16-byte aligned; otherwise (a ragged N, a
+// member boundary, an unaligned output) column by column.
+template <int J>
+__host__ __device__ constexpr int tile_cols() { return kGemmWaves * J * 16; }
+template <int J>
+__host__ __device__ constexpr int tile_pitch() { return tile_cols<J>() + 8; }
+
+template <int J, int MT>
+__device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* tile, int m0) {
+    constexpr int C = tile_cols<J>(), P = tile_pitch<J>();
+    constexpr int kSegs = C / 8, kChunks = 16 * MT * kSegs;
+    const int n_base = blockIdx.x * C;
+    const int rows = a.routed ? a.routes : a.m;
+#pragma unroll
+    for (int i = 0; i < (kChunks + kGemmThreads - 1) / kGemmThreads; ++i) {
+        const int c = threadIdx.x + kGemmThreads * i;
+        if (c >= kChunks) break;
+        const int row = c / kSegs, seg = c % kSegs;
+        const int n = n_base + seg * 8;
+        const int m = a.routed ? a.padded[m0 + row] : m0 + row;
+        if (m >= rows || n >= a.n) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(&tile[row * P + seg * 8]);
+        const int member = n / a.n_member;
+        const int nl = n - member * a.n_member;
+        uint16_t* y = a.ys[member] + (int64_t)m * a.ldys[member] + nl;
+        if (nl + 8 <= a.n_member && n + 8 <= a.n && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+            *reinterpret_cast<uint4*>(y) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            for (int e = 0; e < 8 && n + e < a.n; ++e) {
+                const int ne = n + e, me = ne / a.n_member;
+                a.ys[me][(int64_t)m * a.ldys[me] + (ne - me * a.n_member)] =
+                    (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+    }
+}
 
 // Last arrival of a split-K output block: sums the S partitions of each unit
-// in ascending K order and stores bf16.  Every partition load of a batch of
-// units is in flight at once (the exchange is latency bound, not bandwidth
-// bound); thread t owns units t, t + 256, ...
+// in ascending K order into the LDS output tile.  Every partition load of a
+// batch of units is in flight at once (the exchange is latency bound, not
+// bandwidth bound); thread t owns units t, t + 256, ...
 template <int S, int J, int MT>
-__device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buffer_rsrc_t part,
-                                                int split_bytes, int m0) {
+__device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int split_bytes, uint16_t* tile) {
     constexpr int kPer = J * MT;  // units per thread
     constexpr int kBatch = kPer < 4 ? kPer : 4;
+    constexpr int P = tile_pitch<J>();
 #pragma unroll 1
     for (int b0 = 0; b0 < kPer; b0 += kBatch) {
         floatx4_dev_t v[kBatch][S];
@@ -236,16 +272,10 @@ __device__ __forceinline__ void reduce_partials(const GemmArgs& a, __amdgpu_buff
             const int u = (b0 + b) * kGemmThreads + threadIdx.x;
             const int uw = u / (J * MT * kWave), uj = (u / (MT * kWave)) % J;
             const int umt = (u / kWave) % MT, ul = u % kWave;
-            const int n = ((blockIdx.x * kGemmWaves + uw) * J + uj) * 16 + (ul & 15);
-            if (n >= a.n) continue;
-            const int member = n / a.n_member;
-            uint16_t* y = a.ys[member] + (n - member * a.n_member);
-            const int64_t ldy = a.ldys[member];
+            const int cl = (uw * J + uj) * 16 + (ul & 15);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + umt * 16 + 4 * (ul >> 4) + r;
-                if (m < a.m) y[(int64_t)m * ldy] = (uint16_t)float_to_bf16_bits(sum[r]);
-            }
+            for (int r = 0; r < 4; ++r)
+                tile[(umt * 16 + 4 * (ul >> 4) + r) * P + cl] = (uint16_t)float_to_bf16_bits(sum[r]);
         }
     }
 }
@@ -257,7 +287,10 @@ template <int BITS, int MT, int J, bool G128, bool OCC3 = false>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(OCC3 ? 3 : 1)))
 void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
-    constexpr int S = Stages<BITS, J>::value;
+    // Code/metadata prefetch depth (k-blocks) and activation register stages.
+    // Deeper rings (S = 4, NA up to 4) measured equal on every cfg2 shape: the
+    // loop is not bound by load latency.
+    constexpr int S = 2, NA = 1;
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
     __shared__ float t_lds[128];
     // bits 5..7, G128: per wave, the bf16 levels of its J x 16 columns for the
@@ -340,22 +373,18 @@ void gemm_kernel(GemmArgs a) {
         }
     };
     // activations: 16 * MT rows x 128 k, chunks of 8 bf16; thread t loads
-    // chunk t + kGemmThreads * i (row chunk / 16, k = 8 * (chunk % 16)), i < kAct.
+    // chunk t & 15 (k = 8 * chunk) of rows (t >> 4) + 16 i, i < MT.
     // k % 8 == 0 (admission): a chunk is wholly inside or outside K; rows past
     // M read row M-1 (their outputs are discarded), chunks past K are zero.
-    // With MT = 1 threads also load rows 16..31 (never read by the MFMAs).
-    // Two register stages: the block for kb + 2 is in flight while kb is used.
-    constexpr int kAct = (16 * MT * 16 + kGemmThreads - 1) / kGemmThreads;
-    // One register stage: the block for kb + 1 is in flight while kb is
-    // staged (a second stage measured no faster and costs 16 registers).
-    constexpr int NA = 1;
+    static_assert(kGemmThreads == 256, "one chunk per thread per 16-row block");
+    constexpr int kAct = MT;
     uint4 act[NA][kAct];
     const uint16_t* act_row[kAct];
     int act_r[kAct];
     const int act_c8 = (threadIdx.x & 15) * 8;  // same chunk column for every i
 #pragma unroll
     for (int i = 0; i < kAct; ++i) {
-        act_r[i] = (threadIdx.x + kGemmThreads * i) >> 4;
+        act_r[i] = (threadIdx.x >> 4) + 16 * i;
         act_row[i] = a.x + src_row(act_r[i]) * a.ldx + act_c8;
     }
     // The loaded registers are carried unmodified (any use right after the
@@ -383,14 +412,26 @@ void gemm_kernel(GemmArgs a) {
             constexpr int kStageMask = 1;
             const int ab = st & kStageMask;  // S is even: the stage alternates every block
             uint16_t* lds = a_lds[ab];
-            const uint32_t keep =  // same for all i
-                kb < kb_end && kb * kKBlock + act_c8 < a.k ? 0xFFFFFFFFu : 0u;
+            // a whole k-block inside this split and inside K (wave-uniform)
+            // is stored as loaded; otherwise chunks past K or past the
+            // split's end are zeroed
+            if (kb < kb_end && (kb + 1) * kKBlock <= a.k) {
 #pragma unroll
-            for (int i = 0; i < kAct; ++i) {
-                const int r = act_r[i];
-                const uint4 v = act[st % NA][i];
-                *reinterpret_cast<uint4*>(&lds[((r >> 4) * 256 + a_slot(r & 15, act_c8 >> 3)) * 8]) =
-                    make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+                for (int i = 0; i < kAct; ++i) {
+                    const int r = act_r[i];
+                    *reinterpret_cast<uint4*>(&lds[((r >> 4) * 256 + a_slot(r & 15, act_c8 >> 3)) * 8]) =
+                        act[st % NA][i];
+                }
+            } else {
+                const uint32_t keep =  // same for all i
+                    kb < kb_end && kb * kKBlock + act_c8 < a.k ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+                for (int i = 0; i < kAct; ++i) {
+                    const int r = act_r[i];
+                    const uint4 v = act[st % NA][i];
+                    *reinterpret_cast<uint4*>(&lds[((r >> 4) * 256 + a_slot(r & 15, act_c8 >> 3)) * 8]) =
+                        make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+                }
             }
             uint32_t codes[J][W];
             uint32_t meta[J][MW];
@@ -494,24 +535,23 @@ void gemm_kernel(GemmArgs a) {
     }
 
     // --- epilogue -----------------------------------------------------------
+    // The activation stages are free once every wave is past its last MFMA;
+    // they hold the block's bf16 output tile.
+    uint16_t* tile = &a_lds[0][0];
+    static_assert(16 * MT * tile_pitch<J>() <= 2 * kAStage, "output tile fits the activation stages");
     if (a.split == 1) {
+        constexpr int P = tile_pitch<J>();
+        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int n = (tile0 + j) * 16 + col;
-            if (n >= a.n) continue;
-            const int member = n / a.n_member;
-            uint16_t* y = a.ys[member] + (n - member * a.n_member);
-            const int64_t ldy = a.ldys[member];
+        for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int lr = mt * 16 + 4 * q + r;
-                    const int m = a.routed ? a.padded[m0 + lr] : m0 + lr;
-                    if (m < (a.routed ? a.routes : a.m))
-                        y[(int64_t)m * ldy] = (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
-                }
-        }
+                for (int r = 0; r < 4; ++r)
+                    tile[(mt * 16 + 4 * q + r) * P + (wave * J + j) * 16 + col] =
+                        (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
+        __syncthreads();
+        store_tile<J, MT>(a, tile, m0);
         return;
     }
     // split-K: each workgroup stores its FP32 accumulators in the MFMA-native
@@ -530,16 +570,18 @@ void gemm_kernel(GemmArgs a) {
                           acc[mt][j]);
     __shared__ uint32_t last;
     if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
-    switch (a.split) {
-        case 2: reduce_partials<2, J, MT>(a, part, split_bytes, m0); break;
-        case 3: reduce_partials<3, J, MT>(a, part, split_bytes, m0); break;
-        case 4: reduce_partials<4, J, MT>(a, part, split_bytes, m0); break;
-        case 5: reduce_partials<5, J, MT>(a, part, split_bytes, m0); break;
-        case 6: reduce_partials<6, J, MT>(a, part, split_bytes, m0); break;
-        case 7: reduce_partials<7, J, MT>(a, part, split_bytes, m0); break;
-        default: reduce_partials<8, J, MT>(a, part, split_bytes, m0); break;
+    switch (a.split) {  // arrive_last's barriers leave the stages free
+        case 2: reduce_partials<2, J, MT>(part, split_bytes, tile); break;
+        case 3: reduce_partials<3, J, MT>(part, split_bytes, tile); break;
+        case 4: reduce_partials<4, J, MT>(part, split_bytes, tile); break;
+        case 5: reduce_partials<5, J, MT>(part, split_bytes, tile); break;
+        case 6: reduce_partials<6, J, MT>(part, split_bytes, tile); break;
+        case 7: reduce_partials<7, J, MT>(part, split_bytes, tile); break;
+        default: reduce_partials<8, J, MT>(part, split_bytes, tile); break;
     }
     if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
+    __syncthreads();
+    store_tile<J, MT>(a, tile, m0);
 }
 
 // ---------------------------------------------------------------------------
