@@ -379,61 +379,66 @@ __device__ __forceinline__ void probabilities(const float (&sorted)[SLOTS], floa
     for (int s = 0; s < SLOTS; ++s) out[s] = NORMALIZE ? p[s] / mass : p[s];
 }
 
+// One candidate set of a verified row (which: 0 = q, 1 = p0, 2 = p1), selected
+// and turned into probabilities; ok = every lane's pair is real or padding.
 template <int SLOTS>
-__device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int lane, int64_t* out2) {
+struct VerifySet {
+    LaneSet<SLOTS> sel;
+    float prob[SLOTS];
+    float mass;
+    int count;
+    bool ok;
+};
+
+template <int SLOTS>
+__device__ __forceinline__ void verify_set(const VerifyRow& r, int which, VerifyScratch<SLOTS>& sc, int lane,
+                                           VerifySet<SLOTS>& out) {
     const int block = r.block;
     bool lane_ok = true;
-    LaneSet<SLOTS> qset, p0set, p1set;
+    LaneSet<SLOTS> in;
+    const uint16_t* scores = which == 0 ? r.q_scores : (which == 1 ? r.p0_scores : r.p1_scores);
+    const int64_t* ids = which == 0 ? r.q_ids : (which == 1 ? r.p0_ids : r.p1_ids);
+    const int64_t stride = which == 0 ? r.q_rank_stride : r.p_rank_stride;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
         const int v = lane + kWave * s;
         const bool cm = v < r.tp * r.k;
         const int rank = cm ? v / r.k : 0, local = cm ? v % r.k : 0;
-        const bool load = r.active && cm;
-        const bool load_p = load && r.rows_ok;
-        float qs = -__builtin_huge_valf(), p0s = qs, p1s = qs;
-        int64_t qi = -1, p0i = -1, p1i = -1;
-        if (SLOTS == 1 && r.staged) {
-            if (load) { qs = bf16_bits_to_float(r.st_q_s); qi = r.st_q_i; }
-            if (load_p) {
-                p0s = bf16_bits_to_float(r.st_p0_s); p0i = r.st_p0_i;
-                p1s = bf16_bits_to_float(r.st_p1_s); p1i = r.st_p1_i;
-            }
-        } else {
-            if (load) {
-                qs = bf16_bits_to_float(r.q_scores[rank * r.q_rank_stride + local]);
-                qi = r.q_ids[rank * r.q_rank_stride + local];
-            }
-            if (load_p) {
-                p0s = bf16_bits_to_float(r.p0_scores[rank * r.p_rank_stride + local]);
-                p0i = r.p0_ids[rank * r.p_rank_stride + local];
-                p1s = bf16_bits_to_float(r.p1_scores[rank * r.p_rank_stride + local]);
-                p1i = r.p1_ids[rank * r.p_rank_stride + local];
+        const bool load = r.active && cm && (which == 0 || r.rows_ok);
+        float xs = -__builtin_huge_valf();
+        int64_t xi = -1;
+        if (load) {
+            if (SLOTS == 1 && r.staged) {
+                const uint32_t st_s = which == 0 ? r.st_q_s : (which == 1 ? r.st_p0_s : r.st_p1_s);
+                xs = bf16_bits_to_float(st_s);
+                xi = which == 0 ? r.st_q_i : (which == 1 ? r.st_p0_i : r.st_p1_i);
+            } else {
+                xs = bf16_bits_to_float(scores[rank * stride + local]);
+                xi = ids[rank * stride + local];
             }
         }
-        const bool qr = cm && qi >= 0 && __builtin_fabsf(qs) < __builtin_huge_valf();
-        const bool p0r = cm && p0i >= 0 && __builtin_fabsf(p0s) < __builtin_huge_valf();
-        const bool p1r = cm && p1i >= 0 && __builtin_fabsf(p1s) < __builtin_huge_valf();
-        const bool qpad = cm && qi == -1 && qs != qs;
-        const bool p0pad = cm && p0i == -1 && p0s != p0s;
-        const bool p1pad = cm && p1i == -1 && p1s != p1s;
-        if (v < block)
-            lane_ok = lane_ok && (!cm || qr || qpad) && (!cm || p0r || p0pad) && (!cm || p1r || p1pad);
-        qset.s[s] = qs; qset.i[s] = qi; qset.r[s] = v < block && qr;
-        p0set.s[s] = p0s; p0set.i[s] = p0i; p0set.r[s] = v < block && p0r;
-        p1set.s[s] = p1s; p1set.i[s] = p1i; p1set.r[s] = v < block && p1r;
+        const bool real = cm && xi >= 0 && __builtin_fabsf(xs) < __builtin_huge_valf();
+        const bool pad = cm && xi == -1 && xs != xs;
+        if (v < block) lane_ok = lane_ok && (!cm || real || pad);
+        in.s[s] = xs; in.i[s] = xi; in.r[s] = v < block && real;
     }
-    const bool pairs_valid = __all(lane_ok);
-    LaneSet<SLOTS> q, p0, p1;
-    const int qc = select_set<SLOTS>(qset, block, r.k, lane, sc, q);
-    const int p0c = select_set<SLOTS>(p0set, block, r.k, lane, sc, p0);
-    const int p1c = select_set<SLOTS>(p1set, block, r.k, lane, sc, p1);
+    out.ok = __all(lane_ok);
+    out.count = select_set<SLOTS>(in, block, r.k, lane, sc, out.sel);
+    probabilities<SLOTS>(out.sel.s, r.temperature, r.top_k, r.top_p, block, lane, out.prob, out.mass);
+}
 
-    float qp[SLOTS], p0p[SLOTS], p1p[SLOTS], qm, p0m, p1m;
-    probabilities<SLOTS>(q.s, r.temperature, r.top_k, r.top_p, block, lane, qp, qm);
-    probabilities<SLOTS>(p0.s, r.temperature, r.top_k, r.top_p, block, lane, p0p, p0m);
-    probabilities<SLOTS>(p1.s, r.temperature, r.top_k, r.top_p, block, lane, p1p, p1m);
-
+// Acceptance, the residual draw and the row's decision from its three sets.
+template <int SLOTS>
+__device__ void verify_finish(const VerifyRow& r, const VerifySet<SLOTS>& qs, const VerifySet<SLOTS>& p0s,
+                              const VerifySet<SLOTS>& p1s, VerifyScratch<SLOTS>& sc, int lane, int64_t* out2) {
+    const int block = r.block;
+    const LaneSet<SLOTS>& q = qs.sel;
+    const LaneSet<SLOTS>& p0 = p0s.sel;
+    const LaneSet<SLOTS>& p1 = p1s.sel;
+    const float(&qp)[SLOTS] = qs.prob;
+    const float(&p0p)[SLOTS] = p0s.prob;
+    const float(&p1p)[SLOTS] = p1s.prob;
+    const bool pairs_valid = qs.ok && p0s.ok && p1s.ok;
     float t1[SLOTS], t2[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
@@ -443,16 +448,31 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         if (v < block) { sc.q_id[v] = q.i[s]; sc.q_prob[v] = qp[s]; }
     }
     const float q_draft = vl_tree_sum<SLOTS>(t1, block);
+    const bool greedy = r.temperature == 0.0f;
+    const int64_t p0_top = readlane64(p0.i[0], 0), p1_top = readlane64(p1.i[0], 0);
+    const bool greedy_accepted = r.draft == p0_top;
+    if (greedy) {
+        const bool accepted = greedy_accepted;
+        // a greedy row's decision does not depend on the residual: valid below
+        // reduces to this, and next is the target argmax after the prefix
+        const int64_t need = 1;
+        const bool valid = r.active && pairs_valid && r.rows_ok && r.top_k >= 1 && r.top_k <= r.k &&
+                           r.top_p > 0.0f && r.top_p <= 1.0f && r.seed >= 0 && r.ordinal >= 0 &&
+                           qs.count >= need && p0s.count >= need && p1s.count >= need && qs.mass > 0.0f &&
+                           p0s.mass > 0.0f && p1s.mass > 0.0f && q_draft > 0.0f;
+        if (lane == 0) {
+            out2[0] = valid ? (int64_t)accepted : -1;
+            out2[1] = valid ? (greedy_accepted ? p1_top : p0_top) : -1;
+        }
+        wave_lds_sync();
+        return;
+    }
     const float p_draft = vl_tree_sum<SLOTS>(t2, block);
     const float quotient = p_draft / q_draft;
     const float ratio = quotient < 1.0f ? quotient : 1.0f;
     const uint32_t key = (uint32_t)(r.seed ^ (r.seed >> 32) ^ 0x9E3779B9LL);
     const float u_accept = r.has_uniforms ? r.u0 : philox_uniform(key, (uint32_t)(r.ordinal * 2));
-    const bool random_accepted = u_accept < ratio;
-    const bool greedy = r.temperature == 0.0f;
-    const int64_t p0_top = readlane64(p0.i[0], 0), p1_top = readlane64(p1.i[0], 0);
-    const bool greedy_accepted = r.draft == p0_top;
-    const bool accepted = greedy ? greedy_accepted : random_accepted;
+    const bool accepted = u_accept < ratio;
     wave_lds_sync();
 
     float q_at_p[SLOTS], residual[SLOTS];
@@ -500,8 +520,9 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
     const bool valid = r.active && pairs_valid && r.rows_ok && r.temperature >= 0.0f &&
                        r.temperature < __builtin_huge_valf() && r.top_k >= 1 && r.top_k <= r.k &&
                        r.top_p > 0.0f && r.top_p <= 1.0f && r.seed >= 0 && r.ordinal >= 0 &&
-                       qc >= need && p0c >= need && p1c >= need && qm > 0.0f && p0m > 0.0f &&
-                       p1m > 0.0f && q_draft > 0.0f && (greedy || accepted || rmass > 0.0f);
+                       qs.count >= need && p0s.count >= need && p1s.count >= need && qs.mass > 0.0f &&
+                       p0s.mass > 0.0f && p1s.mass > 0.0f && q_draft > 0.0f &&
+                       (greedy || accepted || rmass > 0.0f);
     const int64_t greedy_next = greedy_accepted ? p1_top : p0_top;
     const int64_t next = greedy ? greedy_next : (accepted ? p1_token : res_token);
     if (lane == 0) {
@@ -509,6 +530,15 @@ __device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int la
         out2[1] = valid ? next : -1;
     }
     wave_lds_sync();
+}
+
+template <int SLOTS>
+__device__ void verify_wave(const VerifyRow& r, VerifyScratch<SLOTS>& sc, int lane, int64_t* out2) {
+    VerifySet<SLOTS> q, p0, p1;
+    verify_set<SLOTS>(r, 0, sc, lane, q);
+    verify_set<SLOTS>(r, 1, sc, lane, p0);
+    verify_set<SLOTS>(r, 2, sc, lane, p1);
+    verify_finish<SLOTS>(r, q, p0, p1, sc, lane, out2);
 }
 
 // --------------------------------------------------------------------------
@@ -714,6 +744,16 @@ __global__ __launch_bounds__(kThreads) void merge_prefix_kernel(const int64_t* d
 // --------------------------------------------------------------------------
 // Candidate tiles + group finalisation (plain candidates or fused verify).
 // --------------------------------------------------------------------------
+// One wave's selected candidate set, handed to the wave that finishes the row.
+struct VerifySetLds {
+    float s[kWave];
+    int64_t i[kWave];
+    float prob[kWave];
+    uint8_t r[kWave];
+    float mass;
+    int count, ok;
+};
+
 struct TileScratch {
     uint32_t survivors[kWaves][kWave] __attribute__((aligned(16)));
     uint32_t wave_top[kWaves * kTop] __attribute__((aligned(16)));
@@ -725,6 +765,7 @@ struct TileScratch {
     int64_t cand_id[9][64];
     int64_t decisions[8][2];
     uint64_t merge[kWaves][kWave];
+    VerifySetLds sets[3];  // one-depth groups: the sets of the three verifying waves
 };
 
 // Inputs of one verified depth (proposal row pi of the fused verify), loaded
@@ -895,30 +936,48 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
 template <int EMAX>
 __device__ bool tile_max(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          int lane, uint32_t* out_top) {
-    uint32_t nonfinite = 0, best = 0;
-    const bool partial = chunks * kChunk > width_left;  // wave-uniform
+    // Per word (two elements): packed order keys, masked to 0 (empty) past the
+    // tile; the word's larger key and the word's position form a composite
+    // whose maximum is the lane's largest key in its lowest word; inside that
+    // word the even element (lower index) wins a tie.
+    // Valid halves of the last chunk (only it can be partial): element
+    // base_idx + (chunks - 1) * kChunk + j exists iff j < lim.
+    const int lim = width_left - (int)base_idx - (chunks - 1) * kChunk;
+    uint32_t last_mask[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+        last_mask[w] = (2 * w < lim ? 0x0000FFFFu : 0u) | (2 * w + 1 < lim ? 0xFFFF0000u : 0u);
+    uint32_t magmax = 0, best = 0;
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const uint32_t word = (&raw[e].x)[w];
-            const uint32_t idx = base_idx + (uint32_t)(e * kChunk + 2 * w);  // low half's element
-            uint32_t valid = e < chunks ? 0xFFFFFFFFu : 0u;
-            if (partial)
-                valid &= ((int)idx < width_left ? 0x0000FFFFu : 0u) | ((int)idx + 1 < width_left ? 0xFFFF0000u : 0u);
-            const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
-            const u16x2_t inf = {0x7F80, 0x7F80};
-            nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
-            const uint32_t k2 = order_key16x2(word) & valid;
-            const uint32_t lo = k2 & 0xFFFFu, hi = k2 >> 16;  // 0 = empty element
-            const uint32_t c0 = lo ? (lo << 16) | (0xFFFFu - idx) : 0u;
-            const uint32_t c1 = hi ? (hi << 16) | (0xFFFEu - idx) : 0u;
-            const uint32_t c = c0 > c1 ? c0 : c1;
+            const uint32_t valid = e < chunks - 1 ? 0xFFFFFFFFu : (e == chunks - 1 ? last_mask[w] : 0u);
+            const uint32_t mag = word & 0x7FFF7FFFu & valid;
+            magmax = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, magmax),
+                                                                            __builtin_bit_cast(u16x2_t, mag)));
+            const uint32_t k2 = order_key16x2(word) & valid;  // 0 = empty element
+            const uint32_t lo = k2 & 0xFFFFu, hi = k2 >> 16;
+            const uint32_t m = lo > hi ? lo : hi;
+            const uint32_t c = (m << 16) | (0xFFFFu - (uint32_t)(e * 4 + w));
             best = c > best ? c : best;
         }
-    best = wave_max_u32(best);
-    if (lane < kTop) out_top[lane] = lane == 0 ? best : 0u;
-    return nonfinite != 0u;
+    // the winning word: its key and which half holds it (lo first)
+    const uint32_t wi = 0xFFFFu - (best & 0xFFFFu), key = best >> 16;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) word = wi == (uint32_t)(e * 4 + w) ? (&raw[e].x)[w] : word;
+    const uint32_t lo_key = order_key16(word & 0xFFFFu);
+    const uint32_t half = lo_key == key ? 0u : 1u;
+    const uint32_t idx = base_idx + (wi >> 2) * kChunk + 2 * (wi & 3) + half;
+    uint32_t lane_best = key ? (key << 16) | (0xFFFFu - idx) : 0u;
+    lane_best = wave_max_u32(lane_best);
+    if (lane < kTop) out_top[lane] = lane == 0 ? lane_best : 0u;
+    const u16x2_t mm = __builtin_bit_cast(u16x2_t, magmax);
+    return mm.x >= 0x7F80 || mm.y >= 0x7F80;
 }
 
 template <int EMAX, bool FUSED, int SLOTS>
@@ -968,7 +1027,11 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     // last workgroup uses them; deeper depths read them when verified)
     const int group = row / a.group_rows;
     VerifyPrefetch pre = {};
-    if (FUSED && wave < a.group_rows - 1) pre = prefetch_verify(a, (int64_t)wave * a.c + group, lane);
+    // (a one-depth group verifies on three waves, each needing depth 0's inputs)
+    const bool split_verify = FUSED && SLOTS == 1 && a.group_rows == 2;
+    const int pre_depth = split_verify ? 0 : wave;
+    if (FUSED && (wave < a.group_rows - 1 || (split_verify && wave < 3)))
+        pre = prefetch_verify(a, (int64_t)pre_depth * a.c + group, lane);
     const bool greedy_row = a.row_temperatures[row] == 0.0f;  // row-uniform
     // wave top-kTop of this wave's share (the maximum alone for a greedy
     // row), then the workgroup's top-kTop
@@ -1010,19 +1073,23 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     for (int gr = wave; gr < a.group_rows; gr += kWaves) {
         const int r = row0 + gr;
         const bool own = r < a.owned_rows;
-        uint32_t bad_row = 0;
-        for (int t = lane; t < a.tiles; t += kWave) bad_row |= load_device(&a.partial_flags[(int64_t)r * a.tiles + t]);
-        bad_row = __any(bad_row != 0);
+        // tiles <= kMaxTiles < 64: one flag per lane; a greedy row's tile
+        // maxima (slot 0) are loaded with it, before either is used
         const float temp = a.row_temperatures[r];
         const bool greedy_pub = temp == 0.0f;
+        const bool tile_lane = lane < a.tiles;
+        uint32_t bad_row = tile_lane ? load_device(&a.partial_flags[(int64_t)r * a.tiles + lane]) : 0u;
+        const uint32_t k32_slot0 =
+            greedy_pub && tile_lane ? load_device(&a.partial_keys[((int64_t)r * a.tiles + lane) * kTop]) : 0u;
+        bad_row = __any(bad_row != 0);
         const int want = a.count < kTop ? a.count : kTop;
         uint64_t my = 0ull;
         if (greedy_pub) {
             // the tiles of a greedy row hold their maximum in slot 0: the
             // row's argmax is the largest of those (lane 0 = rank 0)
             uint64_t e = 0ull;
-            if (lane < a.tiles) {
-                const uint32_t k32 = load_device(&a.partial_keys[((int64_t)r * a.tiles + lane) * kTop]);
+            if (tile_lane) {
+                const uint32_t k32 = k32_slot0;
                 if (k32 != 0u) {
                     const uint32_t id = (uint32_t)lane * (uint32_t)a.tile_width + (0xFFFFu - (k32 & 0xFFFFu));
                     e = ((uint64_t)(k32 >> 16) << 32) | (0xFFFFFFFFu - id);
@@ -1056,12 +1123,18 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
             if (j < a.count && own) {
                 const bool filled = j < want && my != 0ull;
                 const int64_t gid = (int64_t)(0xFFFFFFFFu - (uint32_t)(my & 0xFFFFFFFFu));
+                // the score's bits from its order key, which is one-to-one
+                // except that -0 and +0 share key 0x8000: only then re-read
+                const uint32_t k16 = (uint32_t)(my >> 32);
+                auto exact = [&]() -> uint16_t {
+                    return k16 != 0x8000u ? (uint16_t)key16_to_bf16(k16) : a.logits[(int64_t)r * a.row_stride + gid];
+                };
                 if (bad_row) {
                     id = -2;
                 } else if (!greedy_pub) {
-                    if (filled) { sc = a.logits[(int64_t)r * a.row_stride + gid]; id = gid; }
+                    if (filled) { sc = exact(); id = gid; }
                 } else if (!a.all_random && j == 0 && filled) {
-                    sc = a.logits[(int64_t)r * a.row_stride + gid];
+                    sc = exact();
                     id = gid;
                 }
             }
@@ -1080,14 +1153,13 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __syncthreads();
     // ---- fused: verify each depth of sequence `group`, merge the prefix ----
     const int c = group, depth = a.group_rows - 1;
-    for (int d = wave; d < depth; d += kWaves) {
+    // the verified row of depth d: q candidates from the prefetch (or global),
+    // the target rows d and d + 1 from LDS
+    auto make_row = [&](int d, bool prefetched) {
         const int64_t pi = (int64_t)d * a.c + c;
         VerifyRow vr;
         vr.active = c < a.live_rows;
         vr.rows_ok = true;
-        const bool prefetched = d == wave;  // first depth of this wave
-        // candidates into registers: q from the prefetch (or global), the
-        // target rows d and d + 1 from LDS
         const bool in = lane < a.capacity;
         vr.staged = true;
         vr.st_q_s = prefetched ? pre.q_score : (in ? (uint32_t)a.q_scores[pi * a.capacity + lane] : 0x7FC0u);
@@ -1128,10 +1200,52 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
         vr.has_uniforms = a.uniforms != nullptr;
         vr.underfilled = false;
-        verify_wave<SLOTS>(vr, vs[wave], lane, ts.decisions[d]);
-        if (lane == 0) {
-            a.decisions[2 * pi] = ts.decisions[d][0];
-            a.decisions[2 * pi + 1] = ts.decisions[d][1];
+        return vr;
+    };
+    if (split_verify) {
+        // one depth: waves 0, 1, 2 select and weigh q, p0 and p1 at once; wave
+        // 0 then finishes the row from the three sets (the same operations as
+        // verify_wave, in the same order)
+        const VerifyRow vr = make_row(0, true);
+        if (wave < 3) {
+            VerifySet<SLOTS> mine;
+            verify_set<SLOTS>(vr, wave, vs[wave], lane, mine);
+            VerifySetLds& o = ts.sets[wave];
+            o.s[lane] = mine.sel.s[0];
+            o.i[lane] = mine.sel.i[0];
+            o.r[lane] = mine.sel.r[0];
+            o.prob[lane] = mine.prob[0];
+            if (lane == 0) { o.mass = mine.mass; o.count = mine.count; o.ok = mine.ok; }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            VerifySet<SLOTS> set[3];
+#pragma unroll
+            for (int w = 0; w < 3; ++w) {
+                const VerifySetLds& o = ts.sets[w];
+                set[w].sel.s[0] = o.s[lane];
+                set[w].sel.i[0] = o.i[lane];
+                set[w].sel.r[0] = o.r[lane] != 0;
+                set[w].prob[0] = o.prob[lane];
+                set[w].mass = o.mass;
+                set[w].count = o.count;
+                set[w].ok = o.ok != 0;
+            }
+            verify_finish<SLOTS>(vr, set[0], set[1], set[2], vs[0], lane, ts.decisions[0]);
+            if (lane == 0) {
+                a.decisions[2 * (int64_t)c] = ts.decisions[0][0];
+                a.decisions[2 * (int64_t)c + 1] = ts.decisions[0][1];
+            }
+        }
+    } else {
+        for (int d = wave; d < depth; d += kWaves) {
+            const int64_t pi = (int64_t)d * a.c + c;
+            const VerifyRow vr = make_row(d, d == wave);  // first depth of this wave: prefetched
+            verify_wave<SLOTS>(vr, vs[wave], lane, ts.decisions[d]);
+            if (lane == 0) {
+                a.decisions[2 * pi] = ts.decisions[d][0];
+                a.decisions[2 * pi + 1] = ts.decisions[d][1];
+            }
         }
     }
     __syncthreads();

@@ -280,6 +280,56 @@ __device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int
     }
 }
 
+// Output of one block: split = 1 stores bf16 through the LDS tile; a K split
+// stores the FP32 accumulators in the MFMA-native layout (one 16-byte unit per
+// tile, m-tile and lane) and the last arrival sums the K partitions in
+// ascending order.  `tile` is LDS no longer in use by any wave's main loop.
+template <int J, int MT>
+__device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t (&acc)[MT][J], uint16_t* tile,
+                                             int m0, int wave, int lane) {
+    const int q = lane >> 4, col = lane & 15;
+    if (a.split == 1) {
+        constexpr int P = tile_pitch<J>();
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    tile[(mt * 16 + 4 * q + r) * P + (wave * J + j) * 16 + col] =
+                        (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
+        __syncthreads();
+        store_tile<J, MT>(a, tile, m0);
+        return;
+    }
+    constexpr int kUnits = kGemmWaves * J * MT * kWave;  // float4 units per output block
+    const int block = blockIdx.z * gridDim.x + blockIdx.x;
+    const int split_bytes = (int)(gridDim.x * gridDim.z) * kUnits * 16;  // < 2^31: split > 1 only below 256 blocks of <= 64 KiB
+    const __amdgpu_buffer_rsrc_t part =
+        device_rsrc(reinterpret_cast<char*>(a.partials) + (int64_t)block * kUnits * 16);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            store_device4(part, blockIdx.y * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
+                          acc[mt][j]);
+    __shared__ uint32_t last;
+    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
+    switch (a.split) {  // arrive_last's barriers leave the tile free
+        case 2: reduce_partials<2, J, MT>(part, split_bytes, tile); break;
+        case 3: reduce_partials<3, J, MT>(part, split_bytes, tile); break;
+        case 4: reduce_partials<4, J, MT>(part, split_bytes, tile); break;
+        case 5: reduce_partials<5, J, MT>(part, split_bytes, tile); break;
+        case 6: reduce_partials<6, J, MT>(part, split_bytes, tile); break;
+        case 7: reduce_partials<7, J, MT>(part, split_bytes, tile); break;
+        default: reduce_partials<8, J, MT>(part, split_bytes, tile); break;
+    }
+    if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
+    __syncthreads();
+    store_tile<J, MT>(a, tile, m0);
+}
+
 // OCC3: registers capped for three resident workgroups per CU (the wide
 // single-split launches: lm_head-sized N with J = 2, MT = 4; the cap only
 // spills in the split-K exchange, which those launches do not run).
@@ -537,51 +587,8 @@ void gemm_kernel(GemmArgs a) {
     // --- epilogue -----------------------------------------------------------
     // The activation stages are free once every wave is past its last MFMA;
     // they hold the block's bf16 output tile.
-    uint16_t* tile = &a_lds[0][0];
     static_assert(16 * MT * tile_pitch<J>() <= 2 * kAStage, "output tile fits the activation stages");
-    if (a.split == 1) {
-        constexpr int P = tile_pitch<J>();
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    tile[(mt * 16 + 4 * q + r) * P + (wave * J + j) * 16 + col] =
-                        (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
-        __syncthreads();
-        store_tile<J, MT>(a, tile, m0);
-        return;
-    }
-    // split-K: each workgroup stores its FP32 accumulators in the MFMA-native
-    // layout (one 16-byte unit per tile, m-tile and lane); the last arrival
-    // sums the K partitions in ascending order.
-    constexpr int kUnits = kGemmWaves * J * MT * kWave;  // float4 units per output block
-    const int block = blockIdx.z * gridDim.x + blockIdx.x;
-    const int split_bytes = (int)(gridDim.x * gridDim.z) * kUnits * 16;  // < 2^31: split > 1 only below 256 blocks of <= 64 KiB
-    const __amdgpu_buffer_rsrc_t part =
-        device_rsrc(reinterpret_cast<char*>(a.partials) + (int64_t)block * kUnits * 16);
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            store_device4(part, split * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
-                          acc[mt][j]);
-    __shared__ uint32_t last;
-    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
-    switch (a.split) {  // arrive_last's barriers leave the stages free
-        case 2: reduce_partials<2, J, MT>(part, split_bytes, tile); break;
-        case 3: reduce_partials<3, J, MT>(part, split_bytes, tile); break;
-        case 4: reduce_partials<4, J, MT>(part, split_bytes, tile); break;
-        case 5: reduce_partials<5, J, MT>(part, split_bytes, tile); break;
-        case 6: reduce_partials<6, J, MT>(part, split_bytes, tile); break;
-        case 7: reduce_partials<7, J, MT>(part, split_bytes, tile); break;
-        default: reduce_partials<8, J, MT>(part, split_bytes, tile); break;
-    }
-    if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
-    __syncthreads();
-    store_tile<J, MT>(a, tile, m0);
+    finish_block<J, MT>(a, acc, &a_lds[0][0], m0, wave, lane);
 }
 
 // ---------------------------------------------------------------------------
