@@ -54,7 +54,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // ---------------------------------------------------------------------------
 struct GemmPlan {
     int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
-    int chunk_rows;  // rows per grid-z chunk (64, or 32 when M is split across workgroups)
+    int chunk_rows;  // rows per grid-z chunk (64; 32 when M is split across workgroups; 128 past 64 rows)
     int rows_waves;  // > 0: small-row kernel, this many waves per tile, blocks_per_split per wave
 };
 
@@ -98,7 +98,10 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
         return p;
     }
     plan_k(n_member, k, &p.split, &p.blocks_per_split);
-    const int64_t chunks = ceil_div(m, 64);
+    // Past 64 rows (whole-k-block groups) a workgroup takes 128 rows: each
+    // decoded weight fragment feeds eight m-tiles of MFMA instead of four.
+    const bool wide = m > 64 && group_in % kKBlock == 0;
+    const int64_t chunks = ceil_div(m, wide ? 128 : 64);
     // Two 16-column tiles per wave (half the activation bytes and A-fragment
     // LDS reads per weight byte) when K is whole and the launch still fills the
     // GPU; one tile per wave otherwise.
@@ -107,7 +110,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
     // Rows 33..64 split over two 32-row workgroups when the grid would
     // otherwise hold fewer than two workgroups per CU (qkv, o: measured 7%
     // faster; the weights are read twice, from L2 the second time).
-    p.chunk_rows = 64;
+    p.chunk_rows = wide ? 128 : 64;
     if (p.tiles_per_wave == 1 && m > 32 && m <= 64 && (int64_t)p.col_blocks * p.split < 512)
         p.chunk_rows = 32;
     return p;
@@ -120,9 +123,17 @@ int64_t gemm_workspace(int64_t m, int64_t n_member, int members, int64_t k, int 
     const GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
     if (p.split == 1) return 0;
     const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, p.chunk_rows);
-    const int64_t mt = p.chunk_rows == 32 ? 2 : (ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1)));
+    const int64_t mt = p.chunk_rows == 128 ? 8 : p.chunk_rows == 32 ? 2 : (ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1)));
     const int64_t units = cubic::kGemmWaves * p.tiles_per_wave * mt * 64;
     return align256(blocks * 4) + align256((int64_t)p.split * blocks * units * 16);
+}
+
+// Workspace when the group width is not known yet: the larger of the two
+// chunkings (128-row chunks for whole-k-block groups, 64-row chunks otherwise).
+int64_t gemm_workspace_any_group(int64_t m, int64_t n_member, int members, int64_t k, int bits) {
+    const int64_t a = gemm_workspace(m, n_member, members, k, bits, kKBlock);
+    const int64_t b = gemm_workspace(m, n_member, members, k, bits, 32);
+    return a > b ? a : b;
 }
 
 int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
@@ -342,20 +353,20 @@ int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void
 
 int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits) {
     if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
-    return gemm_workspace(m, n, 1, k, bits, -1);  // group unknown: the MFMA plan bounds both
+    return gemm_workspace_any_group(m, n, 1, k, bits);
 }
 
 int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64_t n, int64_t k, int bits) {
     if (m <= 0 || n <= 0 || k <= 0 || bits < 1 || bits > 8 || members < 1 ||
         members > cubic::kMaxGemmMembers)
         return -1;
-    return gemm_workspace(m, n, members, k, bits, -1);
+    return gemm_workspace_any_group(m, n, members, k, bits);
 }
 
 int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, int64_t k, int bits) {
     if (m <= 0 || n0 <= 0 || n1 <= 0 || k <= 0 || bits < 1 || bits > 8) return -1;
-    if (n0 == n1) return gemm_workspace(m, n0, 2, k, bits, -1);
-    const int64_t w0 = gemm_workspace(m, n0, 1, k, bits, -1), w1 = gemm_workspace(m, n1, 1, k, bits, -1);
+    if (n0 == n1) return gemm_workspace_any_group(m, n0, 2, k, bits);
+    const int64_t w0 = gemm_workspace_any_group(m, n0, 1, k, bits), w1 = gemm_workspace_any_group(m, n1, 1, k, bits);
     return w0 > w1 ? w0 : w1;
 }
 

@@ -39,7 +39,10 @@ constexpr int kKBlock = 128;
 // (lanes 0..15 store rows 0..15 of one chunk) in position r ^ g(c): both run at
 // the b128 peak rate of gfx950's LDS (measured 243 B/clk/CU for the reads,
 // 83 B/clk/CU for the writes; the plain r ^ c swizzle reads at 128).
-constexpr int kAStage = 64 * kKBlock;  // bf16 per stage (64 rows)
+// bf16 per activation stage of a workgroup with MT m-tiles (at least 64 rows:
+// the output tile of the epilogue reuses the stages)
+template <int MT>
+__host__ __device__ constexpr int a_stage() { return (MT > 4 ? MT : 4) * 16 * kKBlock; }
 __device__ __forceinline__ int a_slot(int r16, int c) { return c * 16 + (r16 ^ ((c & 3) << 2) ^ (c >> 2)); }
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -341,6 +344,7 @@ void gemm_kernel(GemmArgs a) {
     // Deeper rings (S = 4, NA up to 4) measured equal on every cfg2 shape: the
     // loop is not bound by load latency.
     constexpr int S = 2, NA = 1;
+    constexpr int kAStage = a_stage<MT>();
     __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][kAStage];
     __shared__ float t_lds[128];
     // bits 5..7, G128: per wave, the bf16 levels of its J x 16 columns for the
@@ -919,6 +923,10 @@ template <int BITS>
 hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t s) {
     if (mt == 1) return launch_j<BITS, 1>(a, j, grid, s);
     if (mt == 2) return launch_j<BITS, 2>(a, j, grid, s);
+    if (mt == 8) {  // 128-row chunks: host plan, whole-k-block groups only
+        if (a.group_in % kKBlock) return hipErrorInvalidValue;
+        return launch_g<BITS, 8, true>(a, j, grid, s);
+    }
     return launch_j<BITS, 4>(a, j, grid, s);
 }
 
@@ -940,7 +948,8 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     // routed: one grid chunk per padded route block (a.m = block capacity)
     const int mt = a.routed ? a.block_m / 16 : (a.m >= 33 ? 4 : (a.m >= 17 ? 2 : 1));
     const int rows_chunks = (a.m + a.chunk_rows - 1) / a.chunk_rows;
-    const int mt_eff = a.routed ? mt : (a.chunk_rows == 32 ? 2 : (rows_chunks == 1 ? mt : 4));
+    const int mt_eff = a.routed ? mt
+                                : (a.chunk_rows == 128 ? 8 : (a.chunk_rows == 32 ? 2 : (rows_chunks == 1 ? mt : 4)));
     const int j = a.tiles_per_wave;  // chosen by the host plan
     const int cols_per_block = kGemmWaves * j * 16;
     dim3 grid((a.n + cols_per_block - 1) / cols_per_block, a.split, rows_chunks);
