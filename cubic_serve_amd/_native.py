@@ -22,18 +22,18 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_last_error": (ctypes.c_char_p, []),
     "cubic_prepared_words": (I32, [I64, I64, I32, I32, P, P]),
     "cubic_prepare_scratch_bytes": (I64, [I64, I64, I32]),
-    "cubic_prepare_weight": (I32, [I32, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P, I64,
+    "cubic_prepare_weight": (I32, [I32, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, I32, P, I64,
                                    P, P, P]),
     "cubic_gemm_workspace_bytes": (I64, [I64, I64, I64, I32]),
     "cubic_gemm_group_workspace_bytes": (I64, [I64, I32, I64, I64, I32]),
     "cubic_gemm_grouped_workspace_bytes": (I64, [I64, I64, I64, I64, I32]),
-    "cubic_gemm_group": (I32, [P, I64, P, P, I64, I32, I64, I64, I32, I32, P, P, P, I64, P]),
-    "cubic_gemm": (I32, [P, I64, P, P, I64, I64, I64, I32, I32, P, I64, P, I64, P]),
-    "cubic_gemm_grouped": (I32, [P, I64, P, P, I64, I64, I64, I64, I32, I32, P, I64, P, I64, P,
+    "cubic_gemm_group": (I32, [P, I64, P, P, I64, I32, I64, I64, I32, I32, I32, P, P, P, I64, P]),
+    "cubic_gemm": (I32, [P, I64, P, P, I64, I64, I64, I32, I32, I32, P, I64, P, I64, P]),
+    "cubic_gemm_grouped": (I32, [P, I64, P, P, I64, I64, I64, I64, I32, I32, I32, P, I64, P, I64, P,
                                  I64, P]),
     "cubic_moe_pad_routes": (I32, [P, P, P, P, P, I32, I32, I32, P, P, P, P]),
     "cubic_moe_max_blocks": (I64, [I64, I32, I32]),
-    "cubic_moe_gemm": (I32, [P, I64, P, P, I64, I64, P, P, P, I64, I32, I32, I32, I64, I64, I32, I32,
+    "cubic_moe_gemm": (I32, [P, I64, P, P, I64, I64, P, P, P, I64, I32, I32, I32, I64, I64, I32, I32, I32,
                              P, I64, P]),
     "cubic_embedding": (I32, [P, I32, I64, I32, P, P, P, P, P, P, P, P, I64, I64, I32, I32, I32, P,
                               I32, P]),

@@ -661,11 +661,12 @@ def save_cubic_checkpoint(root: str | Path, matrices: Mapping[str, QuantizedMatr
     save_file(tensors, str(root / "model.safetensors"))
 
 
-def prepare(matrix: QuantizedMatrix, device: torch.device | str):
-    """Repack a loaded matrix for the gfx950 GEMM (cubic_prepare_weight)."""
+def prepare(matrix: QuantizedMatrix, device: torch.device | str, dtype: torch.dtype = torch.bfloat16):
+    """Repack a loaded matrix for the gfx950 GEMM with `dtype` activations
+    (cubic_prepare_weight)."""
     from .linear import prepare_matrix
 
-    return prepare_matrix(matrix, torch.device(device))
+    return prepare_matrix(matrix, torch.device(device), dtype)
 
 
 __all__ = ["AxisSpan", "CubicCheckpoint", "EncodedWeight", "EncodingRule", "LogicalWeight",

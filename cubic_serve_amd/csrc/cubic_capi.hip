@@ -137,10 +137,11 @@ int64_t gemm_workspace_any_group(int64_t m, int64_t n_member, int members, int64
 }
 
 int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-                int64_t m, int members, int64_t n_member, int64_t k, int bits, int group_in,
+                int64_t m, int members, int64_t n_member, int64_t k, int bits, int group_in, int dtype,
                 void* const* ys, const int64_t* ldys, void* workspace, int64_t workspace_bytes,
                 void* stream) {
     if (!x || !codes || !meta || !ys) return fail(CUBIC_EINVAL, "null operand");
+    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16) return fail(CUBIC_ENOTSUP, "dtype=%d", dtype);
     if (members < 1 || members > cubic::kMaxGemmMembers)
         return fail(CUBIC_EINVAL, "members=%d outside 1..%d", members, cubic::kMaxGemmMembers);
     for (int i = 0; i < members; ++i)
@@ -183,6 +184,7 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
     a.tiles_per_wave = p.tiles_per_wave;
     a.chunk_rows = p.chunk_rows;
     a.rows_waves = p.rows_waves;
+    a.f16 = dtype == CUBIC_DTYPE_F16;
     if (p.split > 1) {
         const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, p.chunk_rows) * 4);  // one per output block
         a.counters = (uint32_t*)workspace;
@@ -301,7 +303,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
 
 extern "C" {
 
-int cubic_abi_version(void) { return 1; }
+int cubic_abi_version(void) { return 2; }
 
 const char* cubic_last_error(void) { return g_error.c_str(); }
 
@@ -324,10 +326,11 @@ int64_t cubic_prepare_scratch_bytes(int64_t n, int64_t k, int group_in) {
 int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void* m1,
                          const void* m2, const void* g0, const void* g1, const void* g2,
                          const int32_t* part_of_row, int64_t n, int64_t k, int bits,
-                         int group_in, int group_out, void* expanded, int64_t expanded_bytes,
+                         int group_in, int group_out, int dtype, void* expanded, int64_t expanded_bytes,
                          uint32_t* codes, uint32_t* meta, void* stream) {
     if (!packed || !m0 || !m1 || !codes || !meta || !expanded)
         return fail(CUBIC_EINVAL, "null operand");
+    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16) return fail(CUBIC_ENOTSUP, "dtype=%d", dtype);
     if (fmt < 0 || fmt > 2) return fail(CUBIC_ENOTSUP, "unknown metadata format %d", fmt);
     if (n <= 0 || k <= 0 || bits < 1 || bits > 8) return fail(CUBIC_EINVAL, "invalid geometry");
     if (group_in <= 0 || group_in % 32) return fail(CUBIC_ENOTSUP, "group_in=%d must be a multiple of 32", group_in);
@@ -347,7 +350,7 @@ int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void
     hipError_t e = cubic::launch_expand_metadata(fmt, m0, m1, m2, g0, g1, g2, part_of_row, n,
                                                  groups_k, group_out, scale, av, bv, s);
     if (e != hipSuccess) return hip_status(e, "metadata expansion");
-    e = cubic::launch_prepare(packed, scale, av, bv, n, k, bits, group_in, codes, meta, s);
+    e = cubic::launch_prepare(packed, scale, av, bv, n, k, bits, group_in, dtype == CUBIC_DTYPE_F16, codes, meta, s);
     return hip_status(e, "weight preparation");
 }
 
@@ -371,25 +374,25 @@ int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, in
 }
 
 int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-               int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
+               int64_t m, int64_t n, int64_t k, int bits, int group_in, int dtype, void* y, int64_t ldy,
                void* workspace, int64_t workspace_bytes, void* stream) {
     void* ys[1] = {y};
     const int64_t ldys[1] = {ldy};
-    return gemm_common(x, ldx, codes, meta, m, 1, n, k, bits, group_in, ys, ldys, workspace,
+    return gemm_common(x, ldx, codes, meta, m, 1, n, k, bits, group_in, dtype, ys, ldys, workspace,
                        workspace_bytes, stream);
 }
 
 int cubic_gemm_group(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-                     int64_t m, int members, int64_t n, int64_t k, int bits, int group_in,
+                     int64_t m, int members, int64_t n, int64_t k, int bits, int group_in, int dtype,
                      void* const* ys, const int64_t* ldys, void* workspace,
                      int64_t workspace_bytes, void* stream) {
     if (!ys || !ldys) return fail(CUBIC_EINVAL, "null output table");
-    return gemm_common(x, ldx, codes, meta, m, members, n, k, bits, group_in, ys, ldys, workspace,
+    return gemm_common(x, ldx, codes, meta, m, members, n, k, bits, group_in, dtype, ys, ldys, workspace,
                        workspace_bytes, stream);
 }
 
 int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
+                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in, int dtype,
                        void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
                        int64_t workspace_bytes, void* stream) {
     if (!y0 || !y1 || n0 <= 0 || n1 <= 0) return fail(CUBIC_EINVAL, "grouped gemm needs two members");
@@ -397,7 +400,7 @@ int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const 
     if (n0 == n1) {
         void* ys[2] = {y0, y1};
         const int64_t ldys[2] = {ldy0, ldy1};
-        return gemm_common(x, ldx, codes, meta, m, 2, n0, k, bits, group_in, ys, ldys, workspace,
+        return gemm_common(x, ldx, codes, meta, m, 2, n0, k, bits, group_in, dtype, ys, ldys, workspace,
                            workspace_bytes, stream);
     }
     // members of different widths have different K plans: one launch each, in
@@ -405,10 +408,10 @@ int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const 
     if (bits < 1 || bits > 8 || group_in <= 0 || group_in % 32 || k <= 0)
         return fail(CUBIC_ENOTSUP, "invalid grouped geometry");
     const int64_t off_c = prepared_code_words(n0 / 16, k, bits), off_m = prepared_meta_words(n0 / 16, k, bits, group_in);
-    const int rc = cubic_gemm(x, ldx, codes, meta, m, n0, k, bits, group_in, y0, ldy0, workspace,
+    const int rc = cubic_gemm(x, ldx, codes, meta, m, n0, k, bits, group_in, dtype, y0, ldy0, workspace,
                               workspace_bytes, stream);
     if (rc != CUBIC_OK) return rc;
-    return cubic_gemm(x, ldx, codes + off_c, meta + off_m, m, n1, k, bits, group_in, y1, ldy1,
+    return cubic_gemm(x, ldx, codes + off_c, meta + off_m, m, n1, k, bits, group_in, dtype, y1, ldy1,
                       workspace, workspace_bytes, stream);
 }
 
@@ -530,9 +533,10 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
                    int64_t expert_code_words, int64_t expert_meta_words, const int32_t* padded,
                    const int32_t* block_expert, const int32_t* padded_total, int64_t max_blocks,
                    int block_m, int routes, int top_k, int64_t n, int64_t k, int bits, int group_in,
-                   void* y, int64_t ldy, void* stream) {
+                   int dtype, void* y, int64_t ldy, void* stream) {
     if (!x || !codes || !meta || !padded || !block_expert || !padded_total || !y)
         return fail(CUBIC_EINVAL, "null operand");
+    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16) return fail(CUBIC_ENOTSUP, "dtype=%d", dtype);
     if (block_m != 16 && block_m != 32 && block_m != 64)
         return fail(CUBIC_ENOTSUP, "block_m=%d not in {16, 32, 64}", block_m);
     if (routes <= 0 || top_k <= 0 || routes % top_k || max_blocks <= 0 || max_blocks * block_m > (1 << 30) ||
@@ -572,6 +576,7 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
     // short route blocks (cfg4: gate/up 76 -> 71 us, down 60 -> 57 us)
     a.tiles_per_wave = 2;
     a.chunk_rows = block_m;
+    a.f16 = dtype == CUBIC_DTYPE_F16;
     a.routed = 1;
     a.block_m = block_m;
     a.padded = padded;

@@ -127,6 +127,7 @@ struct GemmArgs {
     int chunk_rows;               // rows per grid-z chunk: 64, or 32 (M split), or block_m (routed)
     int rows_waves;               // > 0: small-row kernel with this many waves per tile
                                   // (blocks_per_split = k-blocks per wave)
+    int f16;                      // activations, prepared levels and outputs are fp16 (else bf16)
     // routed experts (MoE, routed != 0): workgroup chunk z covers the
     // 16 * MT padded route slots [z * 16 * MT, ...) of one expert
     // (block_expert[z]); a slot holds a route ordinal, or `routes` for
@@ -162,8 +163,9 @@ hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
 hipError_t launch_root_sample(const RootSampleArgs& a, hipStream_t s);
 hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
                                int live_rows, int64_t* out, hipStream_t s);
+// f16: level tables (bits <= 4) in fp16 instead of bf16; codes do not depend on it
 hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t* a,
-                          const uint16_t* b, int64_t n, int64_t k, int bits, int group_in,
+                          const uint16_t* b, int64_t n, int64_t k, int bits, int group_in, int f16,
                           uint32_t* codes, uint32_t* meta, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Routed-block table from compact routes (quantization/common/marlin/repack.py:253-277)

@@ -29,6 +29,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));  // v_cvt_pk_bf16_f32
 }
 
+// Binary32 -> fp16 bits, RNE, of the binary32 value as computed: the empty asm
+// pins the value, so the compiler cannot fold a producing multiply into the
+// conversion (v_fma_mix*_f16 rounds once, where the reference rounds to
+// binary32 and then to fp16; the two differ on ties of the fp16 grid).
+__device__ __forceinline__ uint32_t float_to_f16_bits(float f) {
+    asm volatile("" : "+v"(f));
+    return __half_as_ushort(__float2half_rn(f));
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
@@ -70,8 +79,8 @@ __device__ __forceinline__ void group_metadata(int fmt, const void* m0, const vo
         const float af = (float)(lo >= 8 ? lo - 16 : lo), bf = (float)(hi >= 8 ? hi - 16 : hi);
         scale = (float)si * ((const float*)g0)[p];
         const float prod = af * ((const float*)g1)[p];
-        a = __half_as_ushort(__float2half_rn(1.0f + prod));
-        b = __half_as_ushort(__float2half_rn(bf * ((const float*)g2)[p]));
+        a = (uint16_t)float_to_f16_bits(1.0f + prod);
+        b = (uint16_t)float_to_f16_bits(bf * ((const float*)g2)[p]);
     } else {
         const uint32_t md = ((const uint16_t*)m0)[src];
         scale = half_bits_to_float((md & 0x3FFFu) << 1);

@@ -79,7 +79,7 @@ __device__ __forceinline__ float cubic_value(int raw, const float* t_table, floa
 
 // Output bits of one value (bf16 or fp16, RNE).
 __device__ __forceinline__ uint32_t out_bits(float v, bool fp16) {
-    return fp16 ? (uint32_t)__half_as_ushort(__float2half_rn(v)) : float_to_bf16_bits(v);
+    return fp16 ? float_to_f16_bits(v) : float_to_bf16_bits(v);
 }
 
 // LUT = true (bits <= 4-ish, group_in % 16 == 0, 2^bits * 4 <= group_in): the

@@ -47,6 +47,30 @@ __device__ __forceinline__ int a_slot(int r16, int c) { return c * 16 + (r16 ^ (
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float floatx4_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+
+// Activation / weight / output element type: bf16, or fp16 (F16).  The
+// reference rounds each decoded weight once to the activation dtype and
+// accumulates in FP32 (ops/eager/quantization.py:181-186).
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_level2(float lo, float hi) {
+    if constexpr (F16) return float_to_f16_bits(lo) | (float_to_f16_bits(hi) << 16);
+    else return pack_bf16x2(lo, hi);
+}
+
+template <bool F16>
+__device__ __forceinline__ uint16_t out_bits(float f) {
+    if constexpr (F16) return (uint16_t)float_to_f16_bits(f);
+    else return (uint16_t)float_to_bf16_bits(f);
+}
+
+template <bool F16>
+__device__ __forceinline__ floatx4_t mfma16(uint4 a, uint4 b, floatx4_t c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return __builtin_amdgcn_perm(hi, lo, sel);
@@ -66,7 +90,7 @@ struct LevelTable {
     uint32_t lo_lo, lo_hi, hi_lo, hi_hi;  // low bytes of L0..3, L4..7; high bytes of L0..3, L4..7
 };
 
-template <int BITS>
+template <int BITS, bool F16>
 __device__ __forceinline__ uint32_t level_pair(int m0, float s, float a, float b) {
     // bf16 pair (L[m0], L[m0 + 1]) for the compile-time-unrolled callers below
     float l0, l1;
@@ -78,7 +102,7 @@ __device__ __forceinline__ uint32_t level_pair(int m0, float s, float a, float b
         l0 = m0 < kMags ? curve_level(t_of<BITS>(m0), s, a, b) : 0.0f;
         l1 = m0 + 1 < kMags ? curve_level(t_of<BITS>(m0 + 1), s, a, b) : 0.0f;
     }
-    return pack_bf16x2(l0, l1);
+    return pack_level2<F16>(l0, l1);
 }
 
 __device__ __forceinline__ LevelTable table_from_pairs(uint32_t p0, uint32_t p1, uint32_t p2,
@@ -142,7 +166,7 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t* w, int i) {
     return v & ((1u << BITS) - 1u);
 }
 
-template <int BITS>
+template <int BITS, bool F16>
 __device__ __forceinline__ uint4 direct_fragment(const uint32_t* w, int f, float s, float a,
                                                  float b, const float* t_table) {
     uint32_t out[4];
@@ -157,7 +181,7 @@ __device__ __forceinline__ uint4 direct_fragment(const uint32_t* w, int f, float
             sg[e] = (code >> (BITS - 1)) << 15;
             v[e] = curve_level(t_table[mag], s, a, b);
         }
-        out[h] = pack_bf16x2(v[0], v[1]) ^ (sg[0] | (sg[1] << 16));
+        out[h] = pack_level2<F16>(v[0], v[1]) ^ (sg[0] | (sg[1] << 16));
     }
     return make_uint4(out[0], out[1], out[2], out[3]);
 }
@@ -254,7 +278,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* ti
 // in ascending K order into the LDS output tile.  Every partition load of a
 // batch of units is in flight at once (the exchange is latency bound, not
 // bandwidth bound); thread t owns units t, t + 256, ...
-template <int S, int J, int MT>
+template <int S, int J, int MT, bool F16>
 __device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int split_bytes, uint16_t* tile) {
     constexpr int kPer = J * MT;  // units per thread
     constexpr int kBatch = kPer < 4 ? kPer : 4;
@@ -278,7 +302,7 @@ __device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int
             const int cl = (uw * J + uj) * 16 + (ul & 15);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                tile[(umt * 16 + 4 * (ul >> 4) + r) * P + cl] = (uint16_t)float_to_bf16_bits(sum[r]);
+                tile[(umt * 16 + 4 * (ul >> 4) + r) * P + cl] = out_bits<F16>(sum[r]);
         }
     }
 }
@@ -287,7 +311,7 @@ __device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int
 // stores the FP32 accumulators in the MFMA-native layout (one 16-byte unit per
 // tile, m-tile and lane) and the last arrival sums the K partitions in
 // ascending order.  `tile` is LDS no longer in use by any wave's main loop.
-template <int J, int MT>
+template <int J, int MT, bool F16>
 __device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t (&acc)[MT][J], uint16_t* tile,
                                              int m0, int wave, int lane) {
     const int q = lane >> 4, col = lane & 15;
@@ -301,7 +325,7 @@ __device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t 
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     tile[(mt * 16 + 4 * q + r) * P + (wave * J + j) * 16 + col] =
-                        (uint16_t)float_to_bf16_bits(acc[mt][j][r]);
+                        out_bits<F16>(acc[mt][j][r]);
         __syncthreads();
         store_tile<J, MT>(a, tile, m0);
         return;
@@ -320,13 +344,13 @@ __device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t 
     __shared__ uint32_t last;
     if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
     switch (a.split) {  // arrive_last's barriers leave the tile free
-        case 2: reduce_partials<2, J, MT>(part, split_bytes, tile); break;
-        case 3: reduce_partials<3, J, MT>(part, split_bytes, tile); break;
-        case 4: reduce_partials<4, J, MT>(part, split_bytes, tile); break;
-        case 5: reduce_partials<5, J, MT>(part, split_bytes, tile); break;
-        case 6: reduce_partials<6, J, MT>(part, split_bytes, tile); break;
-        case 7: reduce_partials<7, J, MT>(part, split_bytes, tile); break;
-        default: reduce_partials<8, J, MT>(part, split_bytes, tile); break;
+        case 2: reduce_partials<2, J, MT, F16>(part, split_bytes, tile); break;
+        case 3: reduce_partials<3, J, MT, F16>(part, split_bytes, tile); break;
+        case 4: reduce_partials<4, J, MT, F16>(part, split_bytes, tile); break;
+        case 5: reduce_partials<5, J, MT, F16>(part, split_bytes, tile); break;
+        case 6: reduce_partials<6, J, MT, F16>(part, split_bytes, tile); break;
+        case 7: reduce_partials<7, J, MT, F16>(part, split_bytes, tile); break;
+        default: reduce_partials<8, J, MT, F16>(part, split_bytes, tile); break;
     }
     if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
     __syncthreads();
@@ -336,7 +360,7 @@ __device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t 
 // OCC3: registers capped for three resident workgroups per CU (the wide
 // single-split launches: lm_head-sized N with J = 2, MT = 4; the cap only
 // spills in the split-K exchange, which those launches do not run).
-template <int BITS, int MT, int J, bool G128, bool OCC3 = false>
+template <int BITS, int MT, int J, bool G128, bool OCC3, bool F16>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(OCC3 ? 3 : 1)))
 void gemm_kernel(GemmArgs a) {
     constexpr int W = BITS;  // code words per lane per (tile, k-block)
@@ -529,7 +553,7 @@ void gemm_kernel(GemmArgs a) {
 #pragma unroll
                     for (int p = 0; p < kPer / 2; ++p) {
                         const int m = q * kPer + 2 * p;
-                        pairs[p] = pack_bf16x2(curve_level(t_lds[m], ms[j], ma[j], mb[j]),
+                        pairs[p] = pack_level2<F16>(curve_level(t_lds[m], ms[j], ma[j], mb[j]),
                                                curve_level(t_lds[m + 1], ms[j], ma[j], mb[j]));
                     }
                     uint32_t* dst = reinterpret_cast<uint32_t*>(&lv_lds[((wave * J + j) * 16 + col) * NMP + q * kPer]);
@@ -568,12 +592,10 @@ void gemm_kernel(GemmArgs a) {
                     else if constexpr (LT)
                         bw = table_fragment<BITS>(codes[j], f, &lv_lds[((wave * J + j) * 16 + col) * NMP]);
                     else
-                        bw = direct_fragment<BITS>(codes[j], f, ms[j], ma[j], mb[j], t_lds);
-                    const bf16x8_t bfrag = __builtin_bit_cast(bf16x8_t, bw);
+                        bw = direct_fragment<BITS, F16>(codes[j], f, ms[j], ma[j], mb[j], t_lds);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag_buf[fb][mt], bfrag,
-                                                                             acc[mt][j], 0, 0, 0);
+                        acc[mt][j] = mfma16<F16>(__builtin_bit_cast(uint4, afrag_buf[fb][mt]), bw, acc[mt][j]);
                 }
             }
             // Refill this ring slot only now that its codes are consumed: a load
@@ -592,7 +614,7 @@ void gemm_kernel(GemmArgs a) {
     // The activation stages are free once every wave is past its last MFMA;
     // they hold the block's bf16 output tile.
     static_assert(16 * MT * tile_pitch<J>() <= 2 * kAStage, "output tile fits the activation stages");
-    finish_block<J, MT>(a, acc, &a_lds[0][0], m0, wave, lane);
+    finish_block<J, MT, F16>(a, acc, &a_lds[0][0], m0, wave, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -608,7 +630,7 @@ void gemm_kernel(GemmArgs a) {
 // (quantization/common/small_rows.cu:94-241 and small_rows_cost.py:438-501
 // are the reference's small-row path: a separate arithmetic for M <= 4.)
 // ---------------------------------------------------------------------------
-template <int BITS, int G, int D>
+template <int BITS, int G, int D, bool F16>
 __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
     constexpr int W = BITS;
     constexpr int MW = meta_words<BITS>();
@@ -690,8 +712,7 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
                 const uint4 bw = decode_fragment<BITS>(rc[st], f, tab);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ra[st][f]),
-                                                              __builtin_bit_cast(bf16x8_t, bw), acc, 0, 0, 0);
+                acc = mfma16<F16>(__builtin_bit_cast(uint4, ra[st][f]), bw, acc);
             }
         }
     }
@@ -716,7 +737,7 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
             const int64_t ldy = a.ldys[member];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                if (r < a.m) y[(int64_t)r * ldy] = (uint16_t)float_to_bf16_bits(sum[r]);
+                if (r < a.m) y[(int64_t)r * ldy] = out_bits<F16>(sum[r]);
         }
     }
 }
@@ -724,8 +745,13 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
 template <int BITS>
 hipError_t launch_rows_bits(const GemmArgs& a, int g, hipStream_t s) {
     dim3 grid(a.n_tiles);
-    if (g == 8) rows_kernel<BITS, 8, 4><<<grid, 8 * 64, 0, s>>>(a);
-    else rows_kernel<BITS, 4, 4><<<grid, 4 * 64, 0, s>>>(a);
+    if (a.f16) {
+        if (g == 8) rows_kernel<BITS, 8, 4, true><<<grid, 8 * 64, 0, s>>>(a);
+        else rows_kernel<BITS, 4, 4, true><<<grid, 4 * 64, 0, s>>>(a);
+    } else {
+        if (g == 8) rows_kernel<BITS, 8, 4, false><<<grid, 8 * 64, 0, s>>>(a);
+        else rows_kernel<BITS, 4, 4, false><<<grid, 4 * 64, 0, s>>>(a);
+    }
     return hipGetLastError();
 }
 
@@ -736,7 +762,7 @@ hipError_t launch_rows_bits(const GemmArgs& a, int g, hipStream_t s) {
 // the group's level table as byte planes (lo bytes of L0..3, hi bytes of L0..3,
 // lo bytes of L4..7, hi bytes of L4..7), each level bf16(curve) evaluated in
 // the reference's operation order; bits >= 5: (scale, a | b << 16).
-template <int BITS>
+template <int BITS, bool F16>
 __global__ void prepare_meta_kernel(const float* scale, const uint16_t* av, const uint16_t* bv,
                                     int64_t n, int groups_k, int n_tiles, uint32_t* meta) {
     constexpr int MW = meta_words<BITS>();
@@ -751,10 +777,10 @@ __global__ void prepare_meta_kernel(const float* scale, const uint16_t* av, cons
             const int64_t src = row * groups_k + g;
             if constexpr (BITS <= 4) {
                 const float sc = scale[src], a = half_bits_to_float(av[src]), b = half_bits_to_float(bv[src]);
-                const uint32_t p0 = level_pair<BITS>(0, sc, a, b);
-                const uint32_t p1 = BITS >= 3 ? level_pair<BITS>(2, sc, a, b) : 0u;
-                const uint32_t p2 = BITS >= 4 ? level_pair<BITS>(4, sc, a, b) : 0u;
-                const uint32_t p3 = BITS >= 4 ? level_pair<BITS>(6, sc, a, b) : 0u;
+                const uint32_t p0 = level_pair<BITS, F16>(0, sc, a, b);
+                const uint32_t p1 = BITS >= 3 ? level_pair<BITS, F16>(2, sc, a, b) : 0u;
+                const uint32_t p2 = BITS >= 4 ? level_pair<BITS, F16>(4, sc, a, b) : 0u;
+                const uint32_t p3 = BITS >= 4 ? level_pair<BITS, F16>(6, sc, a, b) : 0u;
                 const LevelTable t = table_from_pairs(p0, p1, p2, p3);
                 w[0] = t.lo_lo; w[1] = t.hi_lo; w[2] = t.lo_hi; w[3] = t.hi_hi;
             } else {
@@ -900,34 +926,39 @@ __global__ void expand_metadata_kernel(int fmt, const void* m0, const void* m1, 
     }
 }
 
-template <int BITS, int MT, bool G128>
+template <int BITS, int MT, bool G128, bool F16>
 hipError_t launch_g(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
-    if constexpr (MT == 4 && BITS <= 5) {
+    if constexpr (MT == 4 && BITS <= 5 && !F16) {
         if (j == 2 && a.split == 1) {
-            gemm_kernel<BITS, MT, 2, G128, true><<<grid, kGemmThreads, 0, s>>>(a);
+            gemm_kernel<BITS, MT, 2, G128, true, F16><<<grid, kGemmThreads, 0, s>>>(a);
             return hipGetLastError();
         }
     }
-    if (j == 2) gemm_kernel<BITS, MT, 2, G128><<<grid, kGemmThreads, 0, s>>>(a);
-    else gemm_kernel<BITS, MT, 1, G128><<<grid, kGemmThreads, 0, s>>>(a);
+    if (j == 2) gemm_kernel<BITS, MT, 2, G128, false, F16><<<grid, kGemmThreads, 0, s>>>(a);
+    else gemm_kernel<BITS, MT, 1, G128, false, F16><<<grid, kGemmThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 
-template <int BITS, int MT>
+template <int BITS, int MT, bool F16>
 hipError_t launch_j(const GemmArgs& a, int j, dim3 grid, hipStream_t s) {
-    if (a.group_in % kKBlock == 0) return launch_g<BITS, MT, true>(a, j, grid, s);
-    return launch_g<BITS, MT, false>(a, j, grid, s);
+    if (a.group_in % kKBlock == 0) return launch_g<BITS, MT, true, F16>(a, j, grid, s);
+    return launch_g<BITS, MT, false, F16>(a, j, grid, s);
+}
+
+template <int BITS, bool F16>
+hipError_t launch_mt(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t s) {
+    if (mt == 1) return launch_j<BITS, 1, F16>(a, j, grid, s);
+    if (mt == 2) return launch_j<BITS, 2, F16>(a, j, grid, s);
+    if (mt == 8) {  // 128-row chunks: host plan, whole-k-block groups only
+        if (a.group_in % kKBlock) return hipErrorInvalidValue;
+        return launch_g<BITS, 8, true, F16>(a, j, grid, s);
+    }
+    return launch_j<BITS, 4, F16>(a, j, grid, s);
 }
 
 template <int BITS>
 hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t s) {
-    if (mt == 1) return launch_j<BITS, 1>(a, j, grid, s);
-    if (mt == 2) return launch_j<BITS, 2>(a, j, grid, s);
-    if (mt == 8) {  // 128-row chunks: host plan, whole-k-block groups only
-        if (a.group_in % kKBlock) return hipErrorInvalidValue;
-        return launch_g<BITS, 8, true>(a, j, grid, s);
-    }
-    return launch_j<BITS, 4>(a, j, grid, s);
+    return a.f16 ? launch_mt<BITS, true>(a, mt, j, grid, s) : launch_mt<BITS, false>(a, mt, j, grid, s);
 }
 
 }  // namespace
@@ -993,7 +1024,7 @@ hipError_t launch_pad_routes(const int32_t* counts, const int32_t* starts, const
 }
 
 hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t* av,
-                          const uint16_t* bv, int64_t n, int64_t k, int bits, int group_in,
+                          const uint16_t* bv, int64_t n, int64_t k, int bits, int group_in, int f16,
                           uint32_t* codes, uint32_t* meta, hipStream_t s) {
     const int n_tiles = (int)((n + 15) / 16);
     const int k_blocks = (int)((k + kKBlock - 1) / kKBlock);
@@ -1014,7 +1045,10 @@ hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t
     const int64_t meta_threads = (int64_t)n_tiles * groups_k * 16;
     const int mblocks = (int)((meta_threads + 255) / 256 < 65535 ? (meta_threads + 255) / 256 : 65535);
     switch (bits) {
-#define CUBIC_META(B) case B: prepare_meta_kernel<B><<<mblocks, 256, 0, s>>>(scale, av, bv, n, groups_k, n_tiles, meta); break;
+#define CUBIC_META(B) case B: \
+        if (f16) prepare_meta_kernel<B, true><<<mblocks, 256, 0, s>>>(scale, av, bv, n, groups_k, n_tiles, meta); \
+        else prepare_meta_kernel<B, false><<<mblocks, 256, 0, s>>>(scale, av, bv, n, groups_k, n_tiles, meta); \
+        break;
         CUBIC_META(1) CUBIC_META(2) CUBIC_META(3) CUBIC_META(4)
         CUBIC_META(5) CUBIC_META(6) CUBIC_META(7) CUBIC_META(8)
 #undef CUBIC_META

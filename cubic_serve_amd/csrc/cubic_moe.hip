@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(MoERouteArgs a
     for (int j = 0; j < k; ++j) out += __shfl(id, j) < id ? 1 : 0;
     if (slot) {
         const float w = p / sum;
-        const uint32_t wb = a.weights_fp16 ? (uint32_t)__half_as_ushort(__float2half_rn(w)) : float_to_bf16_bits(w);
+        const uint32_t wb = a.weights_fp16 ? float_to_f16_bits(w) : float_to_bf16_bits(w);
         a.route_ids[(int64_t)row * k + out] = active ? id : -1;
         a.route_weights[(int64_t)row * k + out] = active ? (uint16_t)wb : (uint16_t)0;
     }

@@ -50,11 +50,15 @@ class PreparedCubic:
     """Format-prepared derivative of one QuantizedMatrix (device-resident)."""
 
     codes: Tensor   # int32 words, MFMA fragment order
-    meta: Tensor    # int32 words, (scale, a | b << 16) per (column, group)
+    meta: Tensor    # int32 words: level tables (bits <= 4) or (scale, a | b << 16) per (column, group)
     n: int
     k: int
     bits: int
     group_in: int
+    dtype: torch.dtype = torch.bfloat16  # activation dtype the level tables are rounded to
+
+
+DTYPE_IDS = {torch.bfloat16: 0, torch.float16: 1}  # CUBIC_DTYPE_BF16 / CUBIC_DTYPE_F16
 
 
 def _versions(matrix: QuantizedMatrix) -> tuple:
@@ -67,10 +71,14 @@ def _versions(matrix: QuantizedMatrix) -> tuple:
     return tuple(versions)
 
 
-def prepare_matrix(matrix: QuantizedMatrix, device: torch.device | None = None) -> PreparedCubic:
-    """Repack a Cubic payload for the gfx950 GEMM (load time, allocates)."""
+def prepare_matrix(matrix: QuantizedMatrix, device: torch.device | None = None,
+                   dtype: torch.dtype = torch.bfloat16) -> PreparedCubic:
+    """Repack a Cubic payload for the gfx950 GEMM with `dtype` activations
+    (load time, allocates)."""
     if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
         raise RuntimeError("Cubic weights require cold preparation before capture")
+    if dtype not in DTYPE_IDS:
+        raise ValueError("Cubic weights serve BF16 or FP16 activations")
     enc = matrix.encoding
     device = torch.device(device) if device is not None else matrix.device
     matrix = matrix.to(device)
@@ -96,10 +104,10 @@ def prepare_matrix(matrix: QuantizedMatrix, device: torch.device | None = None) 
     with torch.cuda.device(device):
         _native.call("cubic_prepare_weight", fmt, p["weight_packed"].data_ptr(),
                      *(_native.ptr(t) for t in tensors), parts.data_ptr(), n, k, enc.bits,
-                     enc.group_in, enc.group_out, scratch.data_ptr(), scratch_bytes,
+                     enc.group_in, enc.group_out, DTYPE_IDS[dtype], scratch.data_ptr(), scratch_bytes,
                      codes.data_ptr(), meta.data_ptr(), _native.stream_of(device))
         torch.cuda.current_stream(device).synchronize()
-    return PreparedCubic(codes, meta, n, k, enc.bits, enc.group_in)
+    return PreparedCubic(codes, meta, n, k, enc.bits, enc.group_in, dtype)
 
 
 def _storage(t: Tensor) -> int:
@@ -142,22 +150,23 @@ class _GemmLaunch:
     def __call__(self, stream: int) -> None:
         x, pr = self.x, self.prepared
         m = x.shape[0]
+        dt = DTYPE_IDS[pr.dtype]
         ws = self.workspace
         ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
         if len(self.outputs) == 1:
             y = self.outputs[0]
             _native.call("cubic_gemm", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
-                         pr.meta.data_ptr(), m, pr.n, pr.k, pr.bits, pr.group_in, y.data_ptr(),
+                         pr.meta.data_ptr(), m, pr.n, pr.k, pr.bits, pr.group_in, dt, y.data_ptr(),
                          y.stride(0), ws_ptr, ws_bytes, stream)
         elif len(set(self.widths)) == 1:
             _native.call("cubic_gemm_group", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
                          pr.meta.data_ptr(), m, len(self.widths), self.widths[0], pr.k, pr.bits,
-                         pr.group_in, self._ys, self._ldys, ws_ptr, ws_bytes, stream)
+                         pr.group_in, dt, self._ys, self._ldys, ws_ptr, ws_bytes, stream)
         else:
             y0, y1 = self.outputs
             _native.call("cubic_gemm_grouped", x.data_ptr(), x.stride(0), pr.codes.data_ptr(),
                          pr.meta.data_ptr(), m, self.widths[0], self.widths[1], pr.k, pr.bits,
-                         pr.group_in, y0.data_ptr(), y0.stride(0), y1.data_ptr(), y1.stride(0),
+                         pr.group_in, dt, y0.data_ptr(), y0.stride(0), y1.data_ptr(), y1.stride(0),
                          ws_ptr, ws_bytes, stream)
 
 
@@ -316,13 +325,14 @@ class PackedLinearOperators:
         self._partitions: dict = {}
 
     # -- preparation -------------------------------------------------------
-    def prepared(self, weights: tuple[QuantizedMatrix, ...], device: torch.device) -> PreparedCubic:
+    def prepared(self, weights: tuple[QuantizedMatrix, ...], device: torch.device,
+                 dtype: torch.dtype = torch.bfloat16) -> PreparedCubic:
         key = ("cubic.mi355x.v1", tuple(id(w) for w in weights), tuple(_versions(w) for w in weights),
-               str(device))
+               str(device), dtype)
         cached = self.prepared_weights.get(key)
         if cached is not None:
             return cached[1]
-        parts = [prepare_matrix(w, device) for w in weights]
+        parts = [prepare_matrix(w, device, dtype) for w in weights]
         if len(parts) == 1:
             prepared = parts[0]
         else:
@@ -330,15 +340,15 @@ class PackedLinearOperators:
             meta = torch.cat([p.meta for p in parts])
             codes = torch.cat([p.codes for p in parts])
             prepared = PreparedCubic(codes, meta, sum(p.n for p in parts), parts[0].k,
-                                     parts[0].bits, parts[0].group_in)
+                                     parts[0].bits, parts[0].group_in, dtype)
         self.prepared_weights[key] = (weights, prepared)
         return prepared
 
     # -- validation (quantized.py:348-405) ------------------------------------
     @staticmethod
     def _validate(x: Tensor, weight: QuantizedMatrix, output: Tensor) -> None:
-        if x.dtype is not torch.bfloat16 or not x.is_cuda:
-            raise ValueError("native linear requires CUDA BF16 activations")
+        if x.dtype not in (torch.float16, torch.bfloat16) or not x.is_cuda:
+            raise ValueError("native linear requires CUDA FP16/BF16 activations")
         if not isinstance(weight, QuantizedMatrix):
             raise TypeError("native Cubic linear requires a packed matrix")
         if weight.device != x.device and weight.device.type != "cpu":
@@ -357,7 +367,7 @@ class PackedLinearOperators:
     def _bind_gemm(self, x: Tensor, weights: tuple, outputs: tuple) -> PackedOperatorBinding:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("Cubic linears must be bound before graph capture")
-        prepared = self.prepared(weights, x.device)
+        prepared = self.prepared(weights, x.device, x.dtype)
         widths = [w.shape[0] for w in weights]
         ws_bytes = gemm_workspace_bytes(x.shape[0], widths, prepared.k, prepared.bits)
         if ws_bytes < 0:
@@ -433,11 +443,11 @@ def bind_prepared(x: Tensor, prepared: PreparedCubic, outputs: Sequence[Tensor],
     widths = tuple(widths) if widths is not None else (prepared.n,)
     if len(widths) != len(outputs) or sum(widths) != prepared.n:
         raise ValueError("grouped widths must cover the prepared columns")
+    if x.dtype is not prepared.dtype or x.ndim != 2 or x.shape[1] != prepared.k:
+        raise ValueError("bound linear requires [M, K] activations of the prepared dtype")
     for y, w in zip(outputs, widths):
-        if y.shape != (x.shape[0], w) or y.dtype is not torch.bfloat16 or not y.is_contiguous():
+        if y.shape != (x.shape[0], w) or y.dtype is not prepared.dtype or not y.is_contiguous():
             raise ValueError("bound linear output has an invalid ABI")
-    if x.dtype is not torch.bfloat16 or x.ndim != 2 or x.shape[1] != prepared.k:
-        raise ValueError("bound linear requires bf16 [M, K] activations")
     ws_bytes = gemm_workspace_bytes(x.shape[0], widths, prepared.k, prepared.bits)
     if ws_bytes < 0:
         raise ValueError("invalid GEMM geometry")
@@ -450,4 +460,4 @@ def bind_prepared(x: Tensor, prepared: PreparedCubic, outputs: Sequence[Tensor],
 def clone_prepared(prepared: PreparedCubic) -> PreparedCubic:
     """A copy in distinct device memory (same values)."""
     return PreparedCubic(prepared.codes.clone(), prepared.meta.clone(), prepared.n, prepared.k,
-                         prepared.bits, prepared.group_in)
+                         prepared.bits, prepared.group_in, prepared.dtype)

@@ -25,7 +25,7 @@ import torch
 from torch import Tensor
 
 from . import _native
-from .linear import PackedLinearOperators, PackedOperatorBinding, prepare_matrix
+from .linear import DTYPE_IDS, PackedLinearOperators, PackedOperatorBinding, prepare_matrix
 from .quantization import QuantizedMatrix
 
 
@@ -209,13 +209,15 @@ class PreparedExperts:
     k: int
     bits: int
     group_in: int
+    dtype: torch.dtype = torch.bfloat16  # activation dtype of the level tables
 
     @property
     def experts(self) -> int:
         return self.codes.shape[0]
 
 
-def prepare_experts(groups: Sequence[Sequence[QuantizedMatrix]], device: torch.device) -> PreparedExperts:
+def prepare_experts(groups: Sequence[Sequence[QuantizedMatrix]], device: torch.device,
+                    dtype: torch.dtype = torch.bfloat16) -> PreparedExperts:
     """Per expert, the group members (gate, up) prepared as one [sum n, k]
     matrix, experts stacked with a fixed stride (load time, allocates)."""
     experts = len(groups[0])
@@ -223,12 +225,13 @@ def prepare_experts(groups: Sequence[Sequence[QuantizedMatrix]], device: torch.d
         raise ValueError("every group needs one matrix per expert")
     codes, meta, first = [], [], None
     for e in range(experts):
-        parts = [prepare_matrix(g[e], device) for g in groups]
+        parts = [prepare_matrix(g[e], device, dtype) for g in groups]
         first = first or parts[0]
         codes.append(torch.cat([p.codes for p in parts]))
         meta.append(torch.cat([p.meta for p in parts]))
     n = sum(g[0].shape[0] for g in groups)
-    return PreparedExperts(torch.stack(codes), torch.stack(meta), n, first.k, first.bits, first.group_in)
+    return PreparedExperts(torch.stack(codes), torch.stack(meta), n, first.k, first.bits, first.group_in,
+                           dtype)
 
 
 class _MoELaunch:
@@ -262,7 +265,7 @@ class _MoELaunch:
                      pr.meta.data_ptr(), pr.codes.shape[1], pr.meta.shape[1], self.padded.data_ptr(),
                      self.block_expert.data_ptr(), self.padded_total.data_ptr(), self.max_blocks,
                      self.block_m, self.routes, self.top_k, pr.n, pr.k, pr.bits, pr.group_in,
-                     self.output.data_ptr(), self.output.stride(0), stream)
+                     DTYPE_IDS[pr.dtype], self.output.data_ptr(), self.output.stride(0), stream)
 
 
 def _admitted(groups, x: Tensor, output: Tensor, params: CubicMoEParameters) -> bool:
@@ -270,7 +273,7 @@ def _admitted(groups, x: Tensor, output: Tensor, params: CubicMoEParameters) -> 
     enc = base.encoding
     return (params.native_enabled and params.block_m in (16, 32, 64) and enc.group_out == 1
             and 1 <= enc.bits <= 8 and enc.group_in % 32 == 0 and base.shape[1] % 8 == 0
-            and x.dtype == torch.bfloat16 and output.dtype == torch.bfloat16
+            and x.dtype in DTYPE_IDS and output.dtype == x.dtype
             and all(w.encoding == enc and w.shape[1] == base.shape[1] and w.shape[0] % 16 == 0
                     for g in groups for w in g))
 
@@ -281,10 +284,10 @@ def _bind(operators: PackedLinearOperators, x: Tensor, groups, output: Tensor, r
         raise RuntimeError("routed Cubic experts must be bound before graph capture")
     if not _admitted(groups, x, output, params):
         return None
-    key = ("cubic.mi355x.moe.v1", tuple(tuple(id(w) for w in g) for g in groups), str(x.device))
+    key = ("cubic.mi355x.moe.v1", tuple(tuple(id(w) for w in g) for g in groups), str(x.device), x.dtype)
     cached = operators.prepared_weights.get(key)
     if cached is None:
-        cached = operators.prepared_weights[key] = (groups, prepare_experts(groups, x.device))
+        cached = operators.prepared_weights[key] = (groups, prepare_experts(groups, x.device, x.dtype))
     prepared = cached[1]
     routes = x.shape[0] * top_k
     if output.shape != (routes, prepared.n) or x.shape[1] != prepared.k:

@@ -39,6 +39,12 @@ extern "C" {
 CUBIC_API int cubic_abi_version(void);
 CUBIC_API const char* cubic_last_error(void);
 
+/* 16-bit floating-point element types of activations, outputs and prepared
+ * level tables (the reference admits FP16 or BF16 activations with the output
+ * in the same dtype: ops/cuda/linear/quantized.py:348-405). */
+#define CUBIC_DTYPE_BF16 0
+#define CUBIC_DTYPE_F16 1
+
 /* ---------------------------------------------------------------------------
  * Cubic weight preparation (load time).
  * Replaces the format-prepared derivatives of quantization/extensions/cubic/
@@ -53,6 +59,9 @@ CUBIC_API const char* cubic_last_error(void);
  *   fmt 1: m0 = weight_scale i8, m1 = weight_ab u8; g0..g2 = *_global f32 [partitions]
  *   fmt 2: m0 = weight_metadata u16; m1 = weight_curve_a f16, m2 = weight_curve_b f16 [partitions, 4]
  *   part_of_row   int32 [n] partition index of each output row (fmt 1, 2; may be NULL for fmt 0)
+ *   dtype         CUBIC_DTYPE_BF16 / _F16: the activation dtype the prepared weight
+ *                 serves (bits <= 4 store per-group level tables rounded to it;
+ *                 the code stream is the same for both)
  *   expanded      device scratch of cubic_prepare_scratch_bytes() bytes
  * Admission (quantization/extensions/cubic/marlin.py:256-336 analogue):
  *   1 <= bits <= 8, group_in % 32 == 0, k % 8 == 0, group_out divides n.
@@ -63,11 +72,13 @@ CUBIC_API int64_t cubic_prepare_scratch_bytes(int64_t n, int64_t k, int group_in
 CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, const void* m1,
                          const void* m2, const void* g0, const void* g1, const void* g2,
                          const int32_t* part_of_row, int64_t n, int64_t k, int bits,
-                         int group_in, int group_out, void* expanded, int64_t expanded_bytes,
-                         uint32_t* codes, uint32_t* meta, void* stream);
+                         int group_in, int group_out, int dtype, void* expanded,
+                         int64_t expanded_bytes, uint32_t* codes, uint32_t* meta, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Cubic WNA16 GEMM: y = x . decode(W)^T, bf16 in/out, FP32 accumulation.
+ * Cubic WNA16 GEMM: y = x . decode(W)^T, bf16 or fp16 in/out (dtype; the
+ * prepared weight must have been prepared for the same dtype), weights
+ * rounded once to that dtype, FP32 accumulation.
  * Replaces the Marlin launch plus _merge_dense_partials of
  * quantization/extensions/cubic/marlin.py:377-521 (bind_planned_linear :339)
  * and the small-row kernel of quantization/common/small_rows.cu:94-241.
@@ -94,7 +105,7 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  *   widths run as one cubic_gemm_group launch; unequal widths run as two
  *   launches (each member keeps its own K plan).  Workspace:
  *   cubic_gemm_grouped_workspace_bytes(m, n0, n1, k, bits).
- * x: bf16 [m, ldx], 16-byte aligned, ldx % 8 == 0.
+ * x: dtype [m, ldx], 16-byte aligned, ldx % 8 == 0; outputs dtype.
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int bits);
 CUBIC_API int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64_t n, int64_t k,
@@ -102,14 +113,14 @@ CUBIC_API int64_t cubic_gemm_group_workspace_bytes(int64_t m, int members, int64
 CUBIC_API int64_t cubic_gemm_grouped_workspace_bytes(int64_t m, int64_t n0, int64_t n1, int64_t k,
                                                      int bits);
 CUBIC_API int cubic_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-               int64_t m, int64_t n, int64_t k, int bits, int group_in, void* y, int64_t ldy,
+               int64_t m, int64_t n, int64_t k, int bits, int group_in, int dtype, void* y, int64_t ldy,
                void* workspace, int64_t workspace_bytes, void* stream);
 CUBIC_API int cubic_gemm_group(const void* x, int64_t ldx, const uint32_t* codes,
                                const uint32_t* meta, int64_t m, int members, int64_t n, int64_t k,
-                               int bits, int group_in, void* const* ys, const int64_t* ldys,
+                               int bits, int group_in, int dtype, void* const* ys, const int64_t* ldys,
                                void* workspace, int64_t workspace_bytes, void* stream);
 CUBIC_API int cubic_gemm_grouped(const void* x, int64_t ldx, const uint32_t* codes, const uint32_t* meta,
-                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in,
+                       int64_t m, int64_t n0, int64_t n1, int64_t k, int bits, int group_in, int dtype,
                        void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
@@ -145,7 +156,7 @@ CUBIC_API int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, 
                              const int32_t* padded, const int32_t* block_expert,
                              const int32_t* padded_total, int64_t max_blocks, int block_m,
                              int routes, int top_k, int64_t n, int64_t k, int bits, int group_in,
-                             void* y, int64_t ldy, void* stream);
+                             int dtype, void* y, int64_t ldy, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Root top-k/top-p sampling of gathered [tp, rows, k] candidates (non-
@@ -184,8 +195,6 @@ CUBIC_API int cubic_root_sample(const void* scores, int scores_fp16, const int64
  * Bit-exact to the reference decode: every value is evaluated in unfused
  * binary32 in the reference's order and rounded once (RNE).
  * ------------------------------------------------------------------------- */
-#define CUBIC_DTYPE_BF16 0
-#define CUBIC_DTYPE_F16 1
 CUBIC_API int cubic_embedding(const void* ids, int id_bytes, int64_t tokens, int fmt,
                               const void* packed, const void* m0, const void* m1, const void* m2,
                               const void* g0, const void* g1, const void* g2,

@@ -12,8 +12,9 @@ unpack_cubic              quantization/extensions/cubic/reference.py:31-47  all-
 pack_cubic                inverse of the above (fixture helper)             round trip with unpack_cubic
 cubic_metadata            reference.py:50-95                                KATs [[1,1],[6,6]] (:154-171) and ones(4,2) (:173-186)
 decode_cubic              reference.py:98-121                               closed form at t in {0,1}; fl32(m/D) exactness; KATs above
+decode_f16                quantization.py:181-182 with FP16 activations     numpy fp32->fp16 cast equals torch's on every decoded value
 linear_bf16               ops/eager/linear.py:43-56 + quantization.py:181  FP64 anchor + enclosure bound
-check_linear_enclosure    guardrail/quantization.py:176-320                 closed form; rejects a +0.25 corruption
+check_linear_enclosure    guardrail/quantization.py:176-320 (bf16, fp16)    closed form; rejects a +0.25 (bf16) / one-ulp-times-8 (fp16) corruption
 candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows
 verify_k1                 ops/cuda/sampling/speculative.py:46-219           reference KATs :73-131, :230-309; frozen-draw sweep :133-228; double-precision _oracle
 root_sample               ops/cuda/sampling/topk_topp.py:22-121             reference oracle KATs tests/ops/test_cuda_topk_topp_sampling.py:65-91 and CUDA-test expectations :127-201; float64 brute force with explicit uniforms
@@ -193,6 +194,15 @@ def decode_bf16(payload: dict, bits: int, metadata: str, shape, group_in: int,
                                          partitions))
 
 
+def decode_f16(payload: dict, bits: int, metadata: str, shape, group_in: int,
+               group_out: int = 1, partitions=()) -> np.ndarray:
+    """Decoded weights rounded once to fp16 (raw uint16 bits): the WNA16 path
+    with FP16 activations (ops/eager/quantization.py:181-182 casts the decoded
+    weight to inputs.dtype); numpy's float32 -> float16 cast is IEEE RNE."""
+    w = decode_cubic(payload, bits, metadata, shape, group_in, group_out, partitions)
+    return w.astype(np.float16).view(np.uint16)
+
+
 # --------------------------------------------------------------------------- #
 # A5/A6: reference linear and its FP64 enclosure
 # --------------------------------------------------------------------------- #
@@ -208,24 +218,32 @@ def linear_bf16(x_bits: np.ndarray, w_bits: np.ndarray):
     return y, y32
 
 
-def check_linear_enclosure(x_bits: np.ndarray, w_bits: np.ndarray, y_bits: np.ndarray) -> dict:
-    """guardrail/quantization.py:250-320 for a bf16 boundary.
+def check_linear_enclosure(x_bits: np.ndarray, w_bits: np.ndarray, y_bits: np.ndarray,
+                           dtype: str = "bf16") -> dict:
+    """guardrail/quantization.py:250-320 for a bf16 or fp16 boundary.
 
     |y - x.w|_f64 <= sum|x||w| (g32 + g64)/(1 - g64) (1 + u) + |anchor| u + tiny*u
     with g32 = s 2^-24 / (1 - s 2^-24), s = k + 12, g64 = k 2^-53 / (1 - k 2^-53),
-    u = eps(bf16)/2.  Raises AssertionError on any excess, like the reference.
+    u = eps(dtype)/2, tiny = the dtype's smallest normal.  Raises
+    AssertionError on any excess, like the reference.
     """
-    x = bf16_bits_to_f32(x_bits).astype(np.float64)
-    w = bf16_bits_to_f32(w_bits).astype(np.float64)
-    y = bf16_bits_to_f32(y_bits).astype(np.float64)
+    if dtype == "bf16":
+        to64 = lambda b: bf16_bits_to_f32(b).astype(np.float64)  # noqa: E731
+        eps, tiny = 2.0**-7, 2.0**-126
+    elif dtype == "f16":
+        to64 = lambda b: _c(b, np.uint16).view(np.float16).astype(np.float64)  # noqa: E731
+        eps, tiny = 2.0**-10, 2.0**-14
+    else:
+        raise ValueError(f"dtype {dtype!r}")
+    x, w, y = to64(x_bits), to64(w_bits), to64(y_bits)
     k = x.shape[1]
     if not (np.isfinite(x).all() and np.isfinite(y).all()):
         raise AssertionError("native linear contains nonfinite operands or outputs")
     steps = k + 12
     gamma32 = steps * 2.0**-24 / (1.0 - steps * 2.0**-24)
     gamma64 = k * 2.0**-53 / (1.0 - k * 2.0**-53)
-    uout = 2.0**-7 / 2.0          # torch.finfo(bfloat16).eps / 2
-    underflow = 2.0**-126 * uout  # torch.finfo(bfloat16).tiny * uout
+    uout = eps / 2.0              # torch.finfo(dtype).eps / 2
+    underflow = tiny * uout       # torch.finfo(dtype).tiny * uout
     anchor = x @ w.T
     bound = (np.abs(x) @ np.abs(w).T) * ((gamma32 + gamma64) / (1.0 - gamma64)) * (1.0 + uout)
     bound += np.abs(anchor) * uout + underflow

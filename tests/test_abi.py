@@ -23,7 +23,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.SIGNATURES), "ctypes signatures drift from the header"
-    assert lib.cubic_abi_version() == 1
+    assert lib.cubic_abi_version() == 2
 
 
 def test_host_planning_entry_points():
@@ -47,7 +47,9 @@ def test_invalid_arguments_fail_before_any_launch():
     with pytest.raises(ValueError, match="tp"):
         _native.call("cubic_verify_candidates", *([16] * 13), 0, 9, 4, 8, 20, 4, 16, None)
     with pytest.raises(ValueError, match="group_in"):
-        _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 100, 16, 4096, None, 0, None)
+        _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 100, 0, 16, 4096, None, 0, None)
+    with pytest.raises(ValueError, match="dtype"):
+        _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 128, 2, 16, 4096, None, 0, None)
     with pytest.raises(ValueError, match="int32 or int64"):
         _native.call("cubic_embedding", 16, 2, 4, 0, 16, 16, 16, 16, None, None, None, None,
                      64, 128, 4, 32, 1, 16, 0, None)

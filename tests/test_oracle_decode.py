@@ -302,3 +302,32 @@ def test_torch_restatement_linear_within_one_bf16_step(oracle):
     _, want = oracle.linear_bf16(xb, wb)
     got = torch_ref.linear_rows(x, w).float().numpy()
     assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 1e-6)
+
+
+def test_f16_decode_and_enclosure(oracle):
+    """FP16 activations: decoded weights round once to fp16 (numpy's cast equals
+    torch's, which the reference uses), and the enclosure takes fp16's unit
+    roundoff: an FP32 dot rounded to fp16 passes, an output moved by eight
+    fp16 ulps fails."""
+    import torch
+    rng = np.random.default_rng(7)
+    n, k = 48, 256
+    groups = n * (k // 128)
+    payload = {"weight_packed": rng.integers(0, 256, (n, k * 4 // 8), dtype=np.uint8),
+               "weight_scale": rng.uniform(0.001, 0.05, (n, k // 128)).astype(np.float32),
+               "weight_a": rng.uniform(0, 1.5, (n, k // 128)).astype(np.float16),
+               "weight_b": rng.uniform(-0.5, 0.5, (n, k // 128)).astype(np.float16)}
+    assert groups == payload["weight_scale"].size
+    w32 = oracle.decode_cubic(payload, 4, "float32-scale-float16-ab", (n, k), 128)
+    wh = oracle.decode_f16(payload, 4, "float32-scale-float16-ab", (n, k), 128)
+    assert np.array_equal(wh, torch.from_numpy(w32).half().view(torch.int16).numpy().view(np.uint16))
+    x = rng.standard_normal((5, k)).astype(np.float16)
+    y32 = x.astype(np.float32) @ wh.view(np.float16).astype(np.float32).T
+    yh = y32.astype(np.float16)
+    report = oracle.check_linear_enclosure(x.view(np.uint16), wh, yh.view(np.uint16), dtype="f16")
+    assert report["max_abs_error"] <= report["max_bound"]
+    bad = yh.copy()
+    i = np.unravel_index(np.argmax(np.abs(bad)), bad.shape)
+    bad[i] = np.float16(float(bad[i]) + 8 * float(np.spacing(bad[i])))
+    with pytest.raises(AssertionError):
+        oracle.check_linear_enclosure(x.view(np.uint16), wh, bad.view(np.uint16), dtype="f16")
