@@ -90,8 +90,10 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  * members equal separate launches bit for bit.
  *
  * cubic_gemm_workspace_bytes: workspace for (m, n, k); 0 when no K split.
- *   The workspace must be zero-filled before its first use; every launch
- *   leaves it zero again.  One workspace per concurrently running launch.
+ *   The workspace must be zero-filled before its first use; every completed
+ *   launch leaves it zero again (a launch killed mid-kernel can leave an
+ *   arrival counter set: zero the workspace again before reusing it).  One
+ *   workspace per concurrently running launch.
  * cubic_gemm: single output y[m, ldy] (columns n).
  * cubic_gemm_group: `members` (1..8) matrices of the same [n, k] shape and
  *   encoding sharing x, prepared as one [members * n, k] matrix (member i's
