@@ -45,6 +45,12 @@ SIGNATURES: dict[str, tuple] = {
                                       I32, I32, P, P]),
     "cubic_root_sample": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P, P]),
     "cubic_merge_prefix": (I32, [P, I32, I32, P, I32, P, P]),
+    "cubic_greedy_workspace_bytes": (I64, [I32, I32]),
+    "cubic_greedy_candidates": (I32, [P, I32, I64, I32, I32, I64, P, P, I64, I32, P, P, P, I64, P]),
+    "cubic_greedy_root": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I64, P, P, P]),
+    "cubic_sampling_final_guard": (I32, [P, P, P, P, P, P, P, P, I32, I32, I64, P, P]),
+    "cubic_greedy_sample": (I32, [P, I32, I64, I32, I32, P, P, I64, I32, P, P, P, P, P, I64, P, P, P,
+                                  P, P, P, I64, P]),
     "cubic_accept_workspace_bytes": (I64, [I32, I32, I32]),
     "cubic_accept": (I32, [P, I64, I32, I32, I32, I32, P, P, P, I32, P, P, P, P, P, P, P, P, P, P,
                            P, P, P, I64, P]),

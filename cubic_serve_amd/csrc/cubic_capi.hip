@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdlib>
 #include <mutex>
+#include <algorithm>
+#include <climits>
 
 #include "cubic_mi355x.h"
 #include "cubic_capi_internal.h"
@@ -697,6 +699,182 @@ int cubic_root_sample(const void* scores, int scores_fp16, const int64_t* ids,
     a.output_tokens = output_tokens;
     a.output_valid = output_valid;
     return hip_status(cubic::launch_root_sample(a, (hipStream_t)stream), "cubic_root_sample launch");
+}
+
+}  // extern "C"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Greedy sampler.  Tiles of whole 2048-column load rounds, as many per row as
+// keep about 2048 workgroups in flight (at most 256, the merge width).
+// ---------------------------------------------------------------------------
+struct GreedyPlan {
+    int tiles, tile_width;
+};
+
+constexpr int64_t kGreedyMaxWidth = int64_t(1) << 30;
+
+GreedyPlan plan_greedy(int rows, int width) {
+    const int64_t w = width > 0 ? width : 1;
+    int64_t want = ceil_div(2048, rows);
+    want = std::min<int64_t>(std::min<int64_t>(want, ceil_div(w, kChunk)), 256);
+    if (want < 1) want = 1;
+    GreedyPlan g;
+    g.tile_width = (int)(ceil_div(ceil_div(w, want), kChunk) * kChunk);
+    g.tiles = (int)ceil_div(w, g.tile_width);
+    return g;
+}
+
+int64_t greedy_workspace(int rows, int width) {
+    const GreedyPlan g = plan_greedy(rows, width);
+    const int64_t slots = (int64_t)rows * g.tiles;
+    return align256(slots * 8) + align256(slots * 4) + align256((int64_t)rows * 4) +
+           align256((int64_t)(rows + 1) * 4);
+}
+
+bool greedy_params(const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                   const int64_t* seeds, const int64_t* ordinals, int k, int64_t vocab_size,
+                   cubic::GreedyParams* p) {
+    if (!temperatures || !top_ps || !top_ks || !seeds || !ordinals) return false;
+    p->temperatures = temperatures;
+    p->top_ps = top_ps;
+    p->top_ks = top_ks;
+    p->seeds = seeds;
+    p->ordinals = ordinals;
+    p->k = k;
+    p->vocab_size = vocab_size;
+    return true;
+}
+
+int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int rows, int width,
+                int64_t vocab_start, const int32_t* metadata, const uint32_t* token_mask,
+                int64_t mask_words, int candidates, void* scores, int64_t* ids, void* workspace,
+                int64_t workspace_bytes, cubic::GreedyArgs& a, const char* who) {
+    if (!logits || !metadata || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "%s: null operand", who);
+    if (rows < 1 || width < 0 || width > kGreedyMaxWidth || row_stride < width)
+        return fail(CUBIC_EINVAL, "%s: invalid logits geometry", who);
+    if (vocab_start < 0) return fail(CUBIC_EINVAL, "%s: negative vocabulary start", who);
+    if (candidates < 1 || candidates > 64) return fail(CUBIC_EINVAL, "%s: need 1 <= candidates <= 64", who);
+    if (token_mask && (mask_words < 1 || vocab_start + width > mask_words * 32))
+        return fail(CUBIC_EINVAL, "%s: grammar mask rows do not cover the visible vocabulary", who);
+    const int64_t need = greedy_workspace(rows, width);
+    if (workspace_bytes < need)
+        return fail(CUBIC_EWORKSPACE, "%s: workspace %lld < %lld", who, (long long)workspace_bytes, (long long)need);
+    const GreedyPlan g = plan_greedy(rows, width);
+    a.logits = (const uint16_t*)logits;
+    a.row_stride = row_stride;
+    a.scores_fp16 = logits_fp16 != 0;
+    a.rows = rows;
+    a.width = width;
+    a.vocab_start = vocab_start;
+    a.metadata = metadata;
+    a.token_mask = token_mask;
+    a.mask_words = mask_words;
+    a.candidates = candidates;
+    a.scores = (uint16_t*)scores;
+    a.ids = ids;
+    a.tiles = g.tiles;
+    a.tile_width = g.tile_width;
+    a.vector_loads = aligned16(logits) && row_stride % 8 == 0;
+    // counters first: their place depends on rows only, so one workspace
+    // serves launches of the same rows at any width it was sized for
+    const int64_t slots = (int64_t)rows * g.tiles;
+    char* w = (char*)workspace;
+    a.counters = (uint32_t*)w;
+    w += align256((int64_t)(rows + 1) * 4);
+    a.row_terms = (uint32_t*)w;
+    w += align256((int64_t)rows * 4);
+    a.partial_keys = (uint64_t*)w;
+    w += align256(slots * 8);
+    a.partial_flags = (uint32_t*)w;
+    return CUBIC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t cubic_greedy_workspace_bytes(int rows, int width) {
+    if (rows < 1 || width < 0 || width > kGreedyMaxWidth) return fail(CUBIC_EINVAL, "invalid greedy geometry");
+    return greedy_workspace(rows, width);
+}
+
+int cubic_greedy_candidates(const void* logits, int logits_fp16, int64_t row_stride, int rows,
+                            int width, int64_t vocab_start, const int32_t* metadata,
+                            const uint32_t* token_mask, int64_t mask_words, int candidates,
+                            void* scores, int64_t* ids, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+    cubic::GreedyArgs a = {};
+    const int rc = greedy_pass(logits, logits_fp16, row_stride, rows, width, vocab_start, metadata,
+                               token_mask, mask_words, candidates, scores, ids, workspace,
+                               workspace_bytes, a, "cubic_greedy_candidates");
+    if (rc != CUBIC_OK) return rc;
+    return hip_status(cubic::launch_greedy(a, (hipStream_t)stream), "cubic_greedy_candidates launch");
+}
+
+int cubic_greedy_root(const void* scores, int scores_fp16, const int64_t* ids,
+                      const float* temperatures, const float* top_ps, const int64_t* top_ks,
+                      const int64_t* seeds, const int64_t* ordinals, const int32_t* metadata,
+                      int tp, int rows, int k, int64_t vocab_size, int64_t* tokens, uint8_t* valid,
+                      void* stream) {
+    cubic::GreedyRootArgs a = {};
+    if (!scores || !ids || !metadata || !tokens || !valid ||
+        !greedy_params(temperatures, top_ps, top_ks, seeds, ordinals, k, vocab_size, &a.p))
+        return fail(CUBIC_EINVAL, "null operand");
+    if (tp < 1 || tp > 8 || k < 1 || k > 64 || rows < 1)
+        return fail(CUBIC_EINVAL, "greedy root needs [TP,C,K] candidates with TP<=8, 1<=K<=64, C>=1");
+    if (vocab_size < 1 || vocab_size > INT32_MAX) return fail(CUBIC_EINVAL, "vocabulary size outside 1..2^31-1");
+    a.scores = (const uint16_t*)scores;
+    a.scores_fp16 = scores_fp16 != 0;
+    a.ids = ids;
+    a.metadata = metadata;
+    a.tp = tp;
+    a.rows = rows;
+    a.tokens = tokens;
+    a.valid = valid;
+    return hip_status(cubic::launch_greedy_root(a, (hipStream_t)stream), "cubic_greedy_root launch");
+}
+
+int cubic_sampling_final_guard(const int64_t* tokens, const uint8_t* root_valid,
+                               const int32_t* metadata, const float* temperatures,
+                               const float* top_ps, const int64_t* top_ks, const int64_t* seeds,
+                               const int64_t* ordinals, int capacity, int k, int64_t vocab_size,
+                               uint8_t* valid, void* stream) {
+    cubic::GuardArgs a = {};
+    if (!tokens || !metadata || !valid ||
+        !greedy_params(temperatures, top_ps, top_ks, seeds, ordinals, k, vocab_size, &a.p))
+        return fail(CUBIC_EINVAL, "null operand");
+    if (capacity < 1 || k < 1) return fail(CUBIC_EINVAL, "final guard needs capacity >= 1 and K >= 1");
+    a.tokens = tokens;
+    a.root_valid = root_valid;
+    a.metadata = metadata;
+    a.capacity = capacity;
+    a.valid = valid;
+    return hip_status(cubic::launch_final_guard(a, (hipStream_t)stream), "cubic_sampling_final_guard launch");
+}
+
+int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride, int rows,
+                        int width, const int32_t* metadata, const uint32_t* token_mask,
+                        int64_t mask_words, int k, const float* temperatures, const float* top_ps,
+                        const int64_t* top_ks, const int64_t* seeds, const int64_t* ordinals,
+                        int64_t vocab_size, void* scores, int64_t* ids, int64_t* tokens,
+                        uint8_t* root_valid, uint8_t* final_valid, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
+    cubic::GreedyArgs a = {};
+    if (!tokens || !root_valid || !final_valid ||
+        !greedy_params(temperatures, top_ps, top_ks, seeds, ordinals, k, vocab_size, &a.p))
+        return fail(CUBIC_EINVAL, "cubic_greedy_sample: null operand");
+    if (vocab_size < 1 || vocab_size > INT32_MAX || width > vocab_size)
+        return fail(CUBIC_EINVAL, "cubic_greedy_sample: visible width exceeds the vocabulary");
+    const int rc = greedy_pass(logits, logits_fp16, row_stride, rows, width, 0, metadata, token_mask,
+                               mask_words, k, scores, ids, workspace, workspace_bytes, a,
+                               "cubic_greedy_sample");
+    if (rc != CUBIC_OK) return rc;
+    a.tokens = tokens;
+    a.root_valid = root_valid;
+    a.final_valid = final_valid;
+    return hip_status(cubic::launch_greedy(a, (hipStream_t)stream), "cubic_greedy_sample launch");
 }
 
 int cubic_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,

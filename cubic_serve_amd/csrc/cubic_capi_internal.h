@@ -158,7 +158,64 @@ struct EmbedArgs {
     int out_fp16;
 };
 
+// Per-row sampling parameters read by the greedy root and the final guard.
+struct GreedyParams {
+    const float* temperatures;    // [rows]
+    const float* top_ps;
+    const int64_t* top_ks;
+    const int64_t* seeds;
+    const int64_t* ordinals;
+    int k;                        // max_top_k (candidates per rank)
+    int64_t vocab_size;           // true vocabulary size
+};
+
+struct GreedyArgs {
+    const uint16_t* logits;       // [rows, row_stride] bf16 or fp16
+    int64_t row_stride;
+    int scores_fp16, rows, width;
+    int64_t vocab_start;
+    const int32_t* metadata;      // [2]: active rows, cancel flag
+    const uint32_t* token_mask;   // [rows, mask_words] or null
+    int64_t mask_words;
+    int candidates;               // published slots per row
+    uint16_t* scores;             // [rows, candidates]
+    int64_t* ids;
+    int tiles, tile_width, vector_loads;
+    uint64_t* partial_keys;       // [rows, tiles]
+    uint32_t* partial_flags;      // [rows, tiles]
+    uint32_t* row_terms;          // [rows] (fused)
+    uint32_t* counters;           // [rows + 1], zero between launches
+    // fused root and guard (tokens == null: candidates only)
+    GreedyParams p;
+    int64_t* tokens;              // [rows]
+    uint8_t* root_valid;          // [rows]
+    uint8_t* final_valid;         // [1]
+};
+
+struct GreedyRootArgs {
+    const uint16_t* scores;       // [tp, rows, k]
+    int scores_fp16;
+    const int64_t* ids;
+    const int32_t* metadata;
+    int tp, rows;
+    GreedyParams p;
+    int64_t* tokens;
+    uint8_t* valid;
+};
+
+struct GuardArgs {
+    const int64_t* tokens;        // [capacity]
+    const uint8_t* root_valid;    // [capacity] or null (not the root rank)
+    const int32_t* metadata;
+    int capacity;
+    GreedyParams p;
+    uint8_t* valid;               // [1]
+};
+
 hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s);
+hipError_t launch_greedy(const GreedyArgs& a, hipStream_t s);
+hipError_t launch_greedy_root(const GreedyRootArgs& a, hipStream_t s);
+hipError_t launch_final_guard(const GuardArgs& a, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
 hipError_t launch_root_sample(const RootSampleArgs& a, hipStream_t s);
 hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,

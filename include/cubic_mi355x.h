@@ -183,6 +183,78 @@ CUBIC_API int cubic_root_sample(const void* scores, int scores_fp16, const int64
                                 int64_t* output_tokens, uint8_t* output_valid, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Greedy sampling for non-speculative decode (CapturedGreedySampler,
+ * ops/cuda/sampling/greedy.py:41-420).  metadata is the sampler's device
+ * int32 [2] = (active rows, cancel flag), read when the launch runs.
+ *
+ * cubic_greedy_candidates replaces greedy_partial + greedy_merge
+ * (greedy.cu:14-78, bound at greedy.py:255-283): per row r < active, the
+ * exact argmax of logits[r, :width] (first maximum, i.e. lowest column, on
+ * ties; -0 == +0) among the columns the grammar mask admits, published as
+ * (score, vocab_start + column) in slot 0 and (NaN, -1) in the other slots.
+ * A row holding any non-finite visible logit (admitted or not) publishes
+ * (NaN, -2) in slot 0; a row the mask empties, rows >= active and width 0
+ * publish (NaN, -1).  Rows >= active read no logits.
+ *   logits       bf16 (logits_fp16 = 0) or fp16 [rows, row_stride]
+ *   token_mask   int32 bit words [rows, mask_words] (bit t%32 of word t/32
+ *                admits token t) or NULL; needs vocab_start + width <= 32 * mask_words
+ *   scores/ids   logits dtype / int64 [rows, candidates], 1 <= candidates <= 64
+ *   workspace    cubic_greedy_workspace_bytes(rows, width) bytes, zero-filled
+ *                once before first use; each launch returns its arrival
+ *                counters to zero; one workspace serves launches of the same
+ *                rows at any width up to the one it was sized for (launches
+ *                sharing a workspace must not overlap)
+ *
+ * cubic_greedy_root replaces greedy_root (greedy.cu:91-114): over gathered
+ * [tp, rows, k] candidates, a row r < active takes the best real candidate
+ * (finite score, 0 <= id < vocab_size; highest score, lowest id on ties) when
+ * every candidate is real or (NaN, -1) padding, at least one is real,
+ * temperature == 0, top_p in (0, 1], 1 <= top_k <= k, seed >= 0 and
+ * ordinal >= 0; tokens[r] = that id and valid[r] = 1, else -1 and 0.  Rows
+ * >= active publish -1 (-2 at row == active when cancelled), valid 0.
+ *   1 <= tp <= 8, 1 <= k <= 64, 1 <= vocab_size <= 2^31 - 1.
+ *
+ * cubic_sampling_final_guard replaces sampling_final_guard (greedy.cu:117-
+ * 139): valid[0] = 0 < active <= capacity and, for every row i < capacity:
+ * i < active: 0 <= tokens[i] < vocab_size, root_valid[i] (skipped when
+ * root_valid is NULL, the reference's non-root ranks), temperature finite in
+ * [0, 2], top_p finite in (0, 1], 1 <= top_k <= k, seed >= 0, ordinal >= 0;
+ * i == active: tokens[i] in {-1, -2}; i > active: tokens[i] == -1.
+ *
+ * cubic_greedy_sample is the single-GPU composition of the three (TP = 1,
+ * vocab_start = 0, candidates = k; the reference's all-gather and broadcast
+ * are identities there) in one launch: the same candidate publication, root
+ * tokens/root_valid and final validity.  width <= vocab_size.
+ * ------------------------------------------------------------------------- */
+CUBIC_API int64_t cubic_greedy_workspace_bytes(int rows, int width);
+CUBIC_API int cubic_greedy_candidates(const void* logits, int logits_fp16, int64_t row_stride,
+                                      int rows, int width, int64_t vocab_start,
+                                      const int32_t* metadata, const uint32_t* token_mask,
+                                      int64_t mask_words, int candidates, void* scores,
+                                      int64_t* ids, void* workspace, int64_t workspace_bytes,
+                                      void* stream);
+CUBIC_API int cubic_greedy_root(const void* scores, int scores_fp16, const int64_t* ids,
+                                const float* temperatures, const float* top_ps,
+                                const int64_t* top_ks, const int64_t* seeds,
+                                const int64_t* ordinals, const int32_t* metadata, int tp, int rows,
+                                int k, int64_t vocab_size, int64_t* tokens, uint8_t* valid,
+                                void* stream);
+CUBIC_API int cubic_sampling_final_guard(const int64_t* tokens, const uint8_t* root_valid,
+                                         const int32_t* metadata, const float* temperatures,
+                                         const float* top_ps, const int64_t* top_ks,
+                                         const int64_t* seeds, const int64_t* ordinals,
+                                         int capacity, int k, int64_t vocab_size, uint8_t* valid,
+                                         void* stream);
+CUBIC_API int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride, int rows,
+                                  int width, const int32_t* metadata, const uint32_t* token_mask,
+                                  int64_t mask_words, int k, const float* temperatures,
+                                  const float* top_ps, const int64_t* top_ks, const int64_t* seeds,
+                                  const int64_t* ordinals, int64_t vocab_size, void* scores,
+                                  int64_t* ids, int64_t* tokens, uint8_t* root_valid,
+                                  uint8_t* final_valid, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
+
+/* ---------------------------------------------------------------------------
  * Packed embedding lookup: out[t, :] = decode(W[ids[t], :]) rounded to the
  * output dtype.  Replaces PackedLinearOperators.bind_embedding for Cubic
  * matrices (ops/cuda/linear/quantized.py:786-846) and the Cubic hook

@@ -23,6 +23,10 @@ moe_compact               ops/cuda/moe/fused.py:174-199                     refe
 merge_prefix              executor/draft_graph.py:146-157                   chain KATs tests/generation/test_tp_sampling.py:120-178
 philox_uniform            guardrail/quantized_graph/speculative.py:15-30    Random123 Philox4x32-10 known-answer vectors
 expf                      (build-fixed exp for the acceptance transform)    <= 2 ulp against libm expf over a dense sweep
+greedy_candidates         ops/cuda/sampling/greedy.cu:14-78                 reference test corpora tests/ops/test_cuda_greedy_sampling.py:95-109 (max + min id) and qualify fixtures greedy.py:640-660; literal column-scan loop on tiny rows (ties, +-0, masks, non-finite)
+greedy_root               ops/cuda/sampling/greedy.cu:91-114                literal per-candidate loop (greedy.cu:94-98 order) on tiny [tp, rows, k]; reference invalid-parameter cases test_cuda_greedy_sampling.py:179-190
+final_guard               ops/cuda/sampling/greedy.cu:117-139               enumerated per-term cases (each predicate flipped alone)
+greedy_sample             greedy.py:255-320 at TP = 1                       composition of the three above
 """
 from __future__ import annotations
 
@@ -385,6 +389,119 @@ def verify_from_logits(logits_bits, q_scores, q_ids, draft_tokens, temperatures,
                            np.asarray(ordinals)[d], live_rows,
                            None if uniforms is None else np.asarray(uniforms)[d])
     return p_scores, p_ids, dec, merge_prefix(dec, live_rows)
+
+
+# --------------------------------------------------------------------------- #
+# Greedy sampler (non-speculative decode)
+# --------------------------------------------------------------------------- #
+NAN_BITS = {"bf16": 0x7FC0, "f16": 0x7E00}   # NaN payload of published padding (not pinned)
+
+
+def _score_values(bits: np.ndarray, fp16: bool) -> np.ndarray:
+    bits = np.asarray(bits, np.uint16)
+    return bits.view(np.float16).astype(np.float64) if fp16 else bf16_bits_to_f32(bits).astype(np.float64)
+
+
+def greedy_candidates(logits_bits, active: int, candidates: int, *, fp16=False, vocab_start=0,
+                      token_mask=None):
+    """greedy_partial + greedy_merge (ops/cuda/sampling/greedy.cu:14-78).
+
+    logits_bits [rows, width] uint16 (bf16 or fp16 bits); token_mask
+    [rows, words] uint32 or None.  Row r < active: the maximum over admitted
+    columns, the lowest column among equal values (float equality, so -0 and
+    +0 tie), published as (score, vocab_start + column) in slot 0; any
+    non-finite visible value (admitted or not) gives (NaN, -2); no admitted
+    column, rows >= active or width 0 give (NaN, -1).  Other slots (NaN, -1).
+    """
+    bits = np.asarray(logits_bits, np.uint16)
+    rows, width = bits.shape
+    vals = _score_values(bits, fp16)
+    nan = NAN_BITS["f16" if fp16 else "bf16"]
+    scores = np.full((rows, candidates), nan, np.uint16)
+    ids = np.full((rows, candidates), -1, np.int64)
+    for r in range(min(active, rows)):
+        if width == 0:
+            continue
+        if not np.isfinite(vals[r]).all():                      # greedy.cu:24, :70
+            ids[r, 0] = -2
+            continue
+        admitted = np.ones(width, bool)
+        if token_mask is not None:                               # greedy.cu:26-27
+            tokens = vocab_start + np.arange(width)
+            words = np.asarray(token_mask, np.uint32)[r][tokens >> 5]
+            admitted = ((words >> (tokens & 31).astype(np.uint32)) & 1).astype(bool)
+        if not admitted.any():                                   # greedy.cu:67
+            continue
+        best = vals[r][admitted].max()
+        col = int(np.flatnonzero(admitted & (vals[r] == best))[0])   # first maximum
+        scores[r, 0] = bits[r, col]
+        ids[r, 0] = vocab_start + col
+    return scores, ids
+
+
+def _greedy_params_ok(t, p, k, seed, ordinal, kmax):
+    return (math.isfinite(p) and 0.0 < p <= 1.0 and 1 <= k <= kmax and seed >= 0 and ordinal >= 0,
+            t == 0.0)
+
+
+def greedy_root(scores_bits, ids, temperatures, top_ps, top_ks, seeds, ordinals, *, active: int,
+                cancel: bool, vocab_size: int, fp16=False):
+    """greedy_root (greedy.cu:91-114) over gathered [tp, rows, k] candidates."""
+    bits = np.asarray(scores_bits, np.uint16)
+    ids = np.asarray(ids, np.int64)
+    tp, rows, k = bits.shape
+    vals = _score_values(bits, fp16)
+    tokens = np.empty(rows, np.int64)
+    valid = np.zeros(rows, bool)
+    for r in range(rows):
+        if r >= active:
+            tokens[r] = -2 if (cancel and r == active) else -1
+            continue
+        s, i = vals[:, r, :].ravel(), ids[:, r, :].ravel()
+        real = np.isfinite(s) & (i >= 0) & (i < vocab_size)
+        sentinel = np.isnan(s) & (i == -1)
+        good = bool((real | sentinel).all())
+        params, greedy = _greedy_params_ok(float(np.float32(temperatures[r])), float(np.float32(top_ps[r])),
+                                           int(top_ks[r]), int(seeds[r]), int(ordinals[r]), k)
+        ok = good and bool(real.any()) and greedy and params
+        if ok:
+            best = s[real].max()
+            tokens[r] = int(i[real & (s == best)].min())
+        else:
+            tokens[r] = -1
+        valid[r] = ok
+    return tokens, valid
+
+
+def final_guard(tokens, root_valid, temperatures, top_ps, top_ks, seeds, ordinals, *, active: int,
+                k: int, vocab_size: int) -> bool:
+    """sampling_final_guard (greedy.cu:117-139); root_valid None = non-root rank."""
+    capacity = len(tokens)
+    good = 0 < active <= capacity
+    for i in range(capacity):
+        tok = int(tokens[i])
+        if i < active:
+            t = float(np.float32(temperatures[i]))
+            params, _ = _greedy_params_ok(0.0, float(np.float32(top_ps[i])), int(top_ks[i]),
+                                          int(seeds[i]), int(ordinals[i]), k)
+            good &= (0 <= tok < vocab_size and (root_valid is None or bool(root_valid[i]))
+                     and math.isfinite(t) and 0.0 <= t <= 2.0 and params)
+        elif i == active:
+            good &= tok in (-1, -2)
+        else:
+            good &= tok == -1
+    return bool(good)
+
+
+def greedy_sample(logits_bits, temperatures, top_ps, top_ks, seeds, ordinals, *, active: int,
+                  cancel: bool, k: int, vocab_size: int, fp16=False, token_mask=None):
+    """Single-GPU composition: candidates -> root -> final guard (TP = 1)."""
+    scores, ids = greedy_candidates(logits_bits, active, k, fp16=fp16, token_mask=token_mask)
+    tokens, valid = greedy_root(scores[None], ids[None], temperatures, top_ps, top_ks, seeds, ordinals,
+                                active=active, cancel=cancel, vocab_size=vocab_size, fp16=fp16)
+    final = final_guard(tokens, valid, temperatures, top_ps, top_ks, seeds, ordinals, active=active,
+                        k=k, vocab_size=vocab_size)
+    return scores, ids, tokens, valid, final
 
 
 if os.environ.get("CUBIC_ORACLE_BUILD_ON_IMPORT") == "1":  # pragma: no cover

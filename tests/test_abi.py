@@ -110,3 +110,26 @@ def test_bench_refuses_more_than_one_gpu():
     assert res.returncode == 2
     assert "one GPU" in res.stderr
     assert res.stdout == ""
+
+
+def test_greedy_sampler_arguments():
+    lib = _native.lib()
+    # one 2048-column tile per row once rows fill the chip; the workspace grows with rows
+    assert 0 < lib.cubic_greedy_workspace_bytes(1, 151936) < lib.cubic_greedy_workspace_bytes(256, 151936)
+    assert lib.cubic_greedy_workspace_bytes(0, 100) == -1
+    ws = lib.cubic_greedy_workspace_bytes(4, 100)
+    with pytest.raises(ValueError, match="candidates"):
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, 65, 16, 16, 16, ws, None)
+    with pytest.raises(ValueError, match="grammar mask"):
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, 16, 3, 20, 16, 16, 16, ws, None)
+    with pytest.raises(ValueError, match="workspace"):
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, 20, 16, 16, 16, ws - 1, None)
+    with pytest.raises(ValueError, match="TP<=8"):
+        _native.call("cubic_greedy_root", 16, 0, 16, 16, 16, 16, 16, 16, 16, 9, 4, 20, 100, 16, 16, None)
+    with pytest.raises(ValueError, match="vocabulary"):
+        _native.call("cubic_greedy_root", 16, 0, 16, 16, 16, 16, 16, 16, 16, 1, 4, 20, 0, 16, 16, None)
+    with pytest.raises(ValueError, match="null"):
+        _native.call("cubic_sampling_final_guard", 16, None, 16, None, 16, 16, 16, 16, 4, 20, 100, 16, None)
+    with pytest.raises(ValueError, match="exceeds the vocabulary"):
+        _native.call("cubic_greedy_sample", 16, 0, 100, 4, 100, 16, None, 0, 20, 16, 16, 16, 16, 16, 99,
+                     16, 16, 16, 16, 16, 16, ws, None)
