@@ -63,6 +63,9 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-only", default=None, choices=("lm_head", "qkv", "o", "gate_up", "down"),
                     help="profiling aid: launch only this GEMM (every layer's copy for the layer "
                          "linears), eagerly, --steps times")
+    ap.add_argument("--greedy-rows", type=int, default=0,
+                    help="profiling aid: time only the greedy sampler over this many rows of "
+                         "Qwen3-8B vocabulary logits and print its JSON")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="profiling aid: run --steps elementwise negations over this many bytes "
                          "(reads and writes each byte once; scales the HBM traffic counters)")
@@ -288,6 +291,7 @@ def measure_extras() -> dict:
     payload) for 64 tokens (one verify step) and 16384 tokens (prefill).
     root_sampler: top-k/top-p sampling of TP=4 x K=20 candidates for 1 and
     256 rows (T 0.8, top-p 0.9, top-k 20).
+    greedy_sampler: greedy sampling from vocabulary logits (measure_greedy).
     checkpoint: one Qwen3-8B-shaped layer loaded from safetensors and
     repacked for the GEMM (measure_checkpoint).
     cfg5: Llama-3-70B-shaped layers, bits x M sweep (measure_cfg5).
@@ -411,9 +415,53 @@ def measure_extras() -> dict:
         ms = time_graph(capture(lambda: [prim.launch(*ops_r) for _ in range(20)]), 10, 2) / 20
         root[f"c{rows}_us"] = round(ms * 1e3, 2)
     out["root_sampler"] = root
+    out["greedy_sampler"] = measure_greedy(dev, g)
     out["checkpoint"] = measure_checkpoint(dev)
     out["cfg5"] = measure_cfg5(dev)
     return out
+
+
+def measure_greedy(dev, g, row_counts=(1, 64, 256)) -> dict:
+    """Greedy sampling of non-speculative decode over the Qwen3-8B vocabulary:
+    the one-launch composition (candidates, root, final guard) for 1, 64 and
+    256 rows of N(0, 3) bf16 logits, and the three separate launches at 64
+    rows.  GB/s = rows x vocab x 2 bytes of logits per launch."""
+    import torch
+
+    from cubic_serve_amd import greedy
+    from cubic_serve_amd.sampling import ShardedSamplingWorkspace
+
+    res = {}
+    for rows in row_counts:
+        logits = (torch.randn((rows, VOCAB), generator=g, device=dev) * 3).to(torch.bfloat16)
+        p = greedy.ShardedSamplingParameters(
+            torch.zeros(rows, device=dev), torch.full((rows,), 20, dtype=torch.int64, device=dev),
+            torch.full((rows,), 0.95, device=dev), 20, torch.ones(rows, dtype=torch.int64, device=dev),
+            torch.zeros(rows, dtype=torch.int64, device=dev))
+        ws = ShardedSamplingWorkspace(torch.empty((rows, 20), dtype=torch.bfloat16, device=dev),
+                                      torch.empty((rows, 20), dtype=torch.int64, device=dev), None, None)
+        plan = greedy.CapturedGreedySampler(
+            local_logits=logits, true_vocab_size=VOCAB, token_ids=torch.empty(rows, dtype=torch.int64, device=dev),
+            parameters=p, workspace=ws, root_valid=torch.empty(rows, dtype=torch.bool, device=dev))
+        tokens = plan.replay(rows).clone()
+        assert torch.equal(tokens, logits.float().argmax(dim=-1)), "greedy tokens differ from argmax"
+        ms = time_graph(capture(lambda: [plan.launch() for _ in range(20)]), 10, 2) / 20
+        res[f"c{rows}_us"] = round(ms * 1e3, 2)
+        res[f"c{rows}_gbs"] = round(rows * VOCAB * 2 / ms / 1e6, 1)
+        if rows == 64:
+            meta, final = plan.metadata, torch.empty((), dtype=torch.bool, device=dev)
+            scratch = greedy.greedy_workspace(rows, VOCAB, dev)
+
+            def three():
+                greedy.greedy_candidates(logits, meta, ws.local_scores, ws.local_token_ids, scratch)
+                greedy.greedy_root(ws.local_scores[None], ws.local_token_ids[None], p, meta,
+                                   plan.token_ids, plan.root_valid, vocab_size=VOCAB)
+                greedy.sampling_final_guard(plan.token_ids, plan.root_valid, meta, p, final,
+                                            vocab_size=VOCAB)
+            ms3 = time_graph(capture(lambda: [three() for _ in range(20)]), 10, 2) / 20
+            res["c64_three_launches_us"] = round(ms3 * 1e3, 2)
+        plan.close()
+    return res
 
 
 def measure_cfg1(dev) -> dict:
@@ -580,6 +628,10 @@ def main(argv=None) -> int:
         for _ in range(args.steps):
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
+        return 0
+    if args.greedy_rows:
+        g = torch.Generator(device="cuda").manual_seed(20)
+        print(json.dumps(measure_greedy(torch.device("cuda:0"), g, (args.greedy_rows,))), flush=True)
         return 0
     step = build_step(args.layers)
     if args.kernel_only:

@@ -706,8 +706,13 @@ int cubic_root_sample(const void* scores, int scores_fp16, const int64_t* ids,
 namespace {
 
 // ---------------------------------------------------------------------------
-// Greedy sampler.  Tiles of whole 2048-column load rounds, as many per row as
-// keep about 2048 workgroups in flight (at most 256, the merge width).
+// Greedy sampler.  Workgroups of 256 threads stream tiles of whole
+// 2048-column load rounds; a row splits into max(4, 256 / rows) tiles, at
+// most 32 (and never more tiles than rounds).  Measured on the Qwen3-8B
+// vocabulary (151936 columns) for 1..256 rows: fewer tiles leave a row's
+// stream latency-bound inside one workgroup, more tiles add workgroups whose
+// fixed cost (parameter loads, reduction, the hand-off to the row's last
+// arrival) exceeds their share of the stream.
 // ---------------------------------------------------------------------------
 struct GreedyPlan {
     int tiles, tile_width;
@@ -717,9 +722,8 @@ constexpr int64_t kGreedyMaxWidth = int64_t(1) << 30;
 
 GreedyPlan plan_greedy(int rows, int width) {
     const int64_t w = width > 0 ? width : 1;
-    int64_t want = ceil_div(2048, rows);
-    want = std::min<int64_t>(std::min<int64_t>(want, ceil_div(w, kChunk)), 256);
-    if (want < 1) want = 1;
+    int64_t want = std::min<int64_t>(std::max<int64_t>(4, ceil_div(256, rows)), 32);
+    want = std::min<int64_t>(want, ceil_div(w, kChunk));
     GreedyPlan g;
     g.tile_width = (int)(ceil_div(ceil_div(w, want), kChunk) * kChunk);
     g.tiles = (int)ceil_div(w, g.tile_width);
@@ -729,8 +733,7 @@ GreedyPlan plan_greedy(int rows, int width) {
 int64_t greedy_workspace(int rows, int width) {
     const GreedyPlan g = plan_greedy(rows, width);
     const int64_t slots = (int64_t)rows * g.tiles;
-    return align256(slots * 8) + align256(slots * 4) + align256((int64_t)rows * 4) +
-           align256((int64_t)(rows + 1) * 4);
+    return align256((int64_t)(rows + 1) * 4) + align256(slots * 8) + align256(slots * 4);
 }
 
 bool greedy_params(const float* temperatures, const float* top_ps, const int64_t* top_ks,
@@ -752,7 +755,7 @@ int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int row
                 int64_t mask_words, int candidates, void* scores, int64_t* ids, void* workspace,
                 int64_t workspace_bytes, cubic::GreedyArgs& a, const char* who) {
     if (!logits || !metadata || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "%s: null operand", who);
-    if (rows < 1 || width < 0 || width > kGreedyMaxWidth || row_stride < width)
+    if (rows < 1 || rows > 65535 || width < 0 || width > kGreedyMaxWidth || row_stride < width)
         return fail(CUBIC_EINVAL, "%s: invalid logits geometry", who);
     if (vocab_start < 0) return fail(CUBIC_EINVAL, "%s: negative vocabulary start", who);
     if (candidates < 1 || candidates > 64) return fail(CUBIC_EINVAL, "%s: need 1 <= candidates <= 64", who);
@@ -783,8 +786,6 @@ int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int row
     char* w = (char*)workspace;
     a.counters = (uint32_t*)w;
     w += align256((int64_t)(rows + 1) * 4);
-    a.row_terms = (uint32_t*)w;
-    w += align256((int64_t)rows * 4);
     a.partial_keys = (uint64_t*)w;
     w += align256(slots * 8);
     a.partial_flags = (uint32_t*)w;
@@ -796,7 +797,8 @@ int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int row
 extern "C" {
 
 int64_t cubic_greedy_workspace_bytes(int rows, int width) {
-    if (rows < 1 || width < 0 || width > kGreedyMaxWidth) return fail(CUBIC_EINVAL, "invalid greedy geometry");
+    if (rows < 1 || rows > 65535 || width < 0 || width > kGreedyMaxWidth)
+        return fail(CUBIC_EINVAL, "invalid greedy geometry");
     return greedy_workspace(rows, width);
 }
 
@@ -867,6 +869,7 @@ int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride,
         return fail(CUBIC_EINVAL, "cubic_greedy_sample: null operand");
     if (vocab_size < 1 || vocab_size > INT32_MAX || width > vocab_size)
         return fail(CUBIC_EINVAL, "cubic_greedy_sample: visible width exceeds the vocabulary");
+    if (rows > 65535) return fail(CUBIC_EINVAL, "cubic_greedy_sample: at most 65535 rows");
     const int rc = greedy_pass(logits, logits_fp16, row_stride, rows, width, 0, metadata, token_mask,
                                mask_words, k, scores, ids, workspace, workspace_bytes, a,
                                "cubic_greedy_sample");

@@ -183,8 +183,8 @@ struct GreedyArgs {
     int tiles, tile_width, vector_loads;
     uint64_t* partial_keys;       // [rows, tiles]
     uint32_t* partial_flags;      // [rows, tiles]
-    uint32_t* row_terms;          // [rows] (fused)
-    uint32_t* counters;           // [rows + 1], zero between launches
+    uint32_t* counters;           // [rows + 1], zero between launches; the last
+                                  // counts fused row arrivals (+ 2^16 per failed guard term)
     // fused root and guard (tokens == null: candidates only)
     GreedyParams p;
     int64_t* tokens;              // [rows]
