@@ -21,6 +21,11 @@ LIB = LIB_DIR / "libcubic_mi355x.so"
 SOURCES = ("cubic_capi.hip", "cubic_gemm.hip", "cubic_accept.hip", "cubic_embed.hip", "cubic_moe.hip",
            "cubic_greedy.hip")
 ARCH = "gfx950"
+# Per-source flags.  The acceptance kernel sizes its LDS for three workgroups
+# per CU (three waves per SIMD at its register count); LLVM's promotion of
+# small private arrays to LDS would add 3 KB per workgroup and leave room for
+# two, so that promotion is off for this file (the arrays stay in registers).
+FILE_FLAGS = {"cubic_accept.hip": ("-mllvm", "-disable-promote-alloca-to-lds")}
 
 
 def hipcc() -> str:
@@ -51,7 +56,7 @@ def build(verbose: bool = False, jobs: int = 3) -> Path:
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         objects.append(obj)
-        cmd = [cc, *flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *flags(), *FILE_FLAGS.get(src, ()), "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

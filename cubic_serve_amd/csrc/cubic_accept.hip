@@ -18,6 +18,8 @@
 // Wave-level reductions follow fixed orders (butterfly sums in ascending
 // lane distance, row-wise scans; cubic_device.h) that the CPU restatement
 // reproduces operation for operation.
+#include <type_traits>
+
 #include "cubic_device.h"
 #include "cubic_capi_internal.h"
 
@@ -757,7 +759,6 @@ struct VerifySetLds {
 struct TileScratch {
     uint32_t survivors[kWaves][kWave] __attribute__((aligned(16)));
     uint32_t wave_top[kWaves * kTop] __attribute__((aligned(16)));
-    uint32_t tile_top[kTop];
     uint32_t flags[kWaves];
     uint32_t last;
     // finalisation: candidates of the group rows (count <= 64, rows <= 9)
@@ -806,41 +807,67 @@ __device__ __forceinline__ uint32_t elem_composite(const uint4 (&raw)[EMAX], int
     return (order_key16(u) << 16) | (0xFFFFu - (uint32_t)idx);
 }
 
+// Prefilter key of a bf16 pair, one per half: the bits with the sign bit
+// flipped for positive values and all bits flipped for negative ones (three
+// VALU per word).  It orders like the values except that -0 (0x7FFF) sits
+// just below +0 (0x8000), where the exact order ties them; inf and positive
+// NaN map to >= 0xFF80, -inf and negative NaN to <= 0x007F.
+__device__ __forceinline__ uint32_t prefilter_key2(uint32_t w) {
+    const uint32_t s = __builtin_bit_cast(uint32_t, (i16x2_t)(__builtin_bit_cast(i16x2_t, w) >> 15));
+    return w ^ (s | 0x80008000u);
+}
+// Exact order key (order_key16) of a nonzero 16-bit prefilter key.
+__device__ __forceinline__ uint32_t exact_of_prefilter(uint32_t k) {
+    const uint32_t raw = k >= 0x8000u ? k ^ 0x8000u : (~k & 0xFFFFu);
+    return order_key16(raw);
+}
+
 // Returns whether any element of the lane's share is non-finite.
 template <int EMAX>
 __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          TileScratch& ts, uint32_t* kw, int lane, int wave, uint32_t* out_top) {
-    // 1. order keys, two per word (elements 2w, 2w + 1 of a chunk), 0 = empty;
-    //    a half is non-finite iff its magnitude is >= 0x7F80
+    // 1. prefilter keys, two per word (elements 2w, 2w + 1 of a chunk), 0 =
+    //    empty; the lane maximum and, for whole tiles, the lane minimum: a
+    //    whole tile is non-finite iff its extreme keys reach the inf/NaN ranges
     uint32_t key2[EMAX][4];
     uint32_t nonfinite = 0;
-    const bool partial = chunks * kChunk > width_left;  // wave-uniform
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t word = (&raw[e].x)[w];
-            uint32_t valid = e < chunks ? 0xFFFFFFFFu : 0u;
-            if (partial) {
-                const int idx = (int)base_idx + e * kChunk + 2 * w;
-                valid &= (idx < width_left ? 0x0000FFFFu : 0u) | (idx + 1 < width_left ? 0xFFFF0000u : 0u);
-            }
-            const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
-            const u16x2_t inf = {0x7F80, 0x7F80};
-            nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
-            key2[e][w] = order_key16x2(word) & valid;
-        }
-    // 2. lane maxima (packed), then tau16 = the kTop-th largest lane maximum
-    //    (ballot radix select): kTop lanes hold distinct elements of value
-    //    >= tau16, so every element of the top kTop has a key >= tau16.
+    const bool whole = chunks == EMAX && chunks * kChunk <= width_left;  // wave-uniform
     u16x2_t m2 = {0, 0};
+    if (whole) {
+        u16x2_t n2 = {0xFFFF, 0xFFFF};
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e)
+        for (int e = 0; e < EMAX; ++e)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const u16x2_t k = __builtin_bit_cast(u16x2_t, key2[e][w]);
-            m2 = k > m2 ? k : m2;
-        }
+            for (int w = 0; w < 4; ++w) {
+                key2[e][w] = prefilter_key2((&raw[e].x)[w]);
+                const u16x2_t k = __builtin_bit_cast(u16x2_t, key2[e][w]);
+                m2 = __builtin_elementwise_max(m2, k);
+                n2 = __builtin_elementwise_min(n2, k);
+            }
+        nonfinite = (m2.x >= 0xFF80u) | (m2.y >= 0xFF80u) | (n2.x <= 0x007Fu) | (n2.y <= 0x007Fu);
+    } else {
+        const bool partial = chunks * kChunk > width_left;  // wave-uniform
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t word = (&raw[e].x)[w];
+                uint32_t valid = e < chunks ? 0xFFFFFFFFu : 0u;
+                if (partial) {
+                    const int idx = (int)base_idx + e * kChunk + 2 * w;
+                    valid &= (idx < width_left ? 0x0000FFFFu : 0u) | (idx + 1 < width_left ? 0xFFFF0000u : 0u);
+                }
+                const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
+                const u16x2_t inf = {0x7F80, 0x7F80};
+                nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
+                key2[e][w] = prefilter_key2(word) & valid;
+                m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2_t, key2[e][w]));
+            }
+    }
+    // 2. tau = the kTop-th largest lane maximum (ballot radix select): kTop
+    //    lanes hold distinct elements with keys >= tau, so every element of
+    //    the exact top kTop has a prefilter key >= tau -- or is -0 (0x7FFF)
+    //    tied with a +0 tau (0x8000), which the threshold then admits too.
     const uint32_t lane_max = m2.x > m2.y ? m2.x : m2.y;
     uint32_t tau = 0;
 #pragma unroll
@@ -848,15 +875,17 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
         const uint32_t cand = tau | (1u << b);
         if (__popcll(__ballot(lane_max >= cand)) >= kTop) tau = cand;
     }
-    const uint32_t thr = tau > 0u ? tau : 1u;  // empty elements never survive
-    // 3. compact survivors (key >= thr) as composites.  Each lane marks the
-    //    words holding a survivor (saturating packed subtract: nonzero iff a
-    //    half is >= thr) and spills its keys to LDS word-major (lane-distinct
-    //    banks); the wave then takes one marked word per lane per round, so
-    //    the rounds number the largest per-lane count of marked words, not
-    //    the words.  Survivor order is irrelevant: ranks count composites.
+    const uint32_t thr = tau == 0x8000u ? 0x7FFFu : (tau > 0u ? tau : 1u);  // empty never survives
+    // 3. compact survivors (prefilter key >= thr) as exact composites.  Each
+    //    lane marks the words holding a survivor (saturating packed subtract:
+    //    nonzero iff a half is >= thr) and spills its keys to LDS word-major
+    //    (lane-distinct banks); the wave then takes one marked word per lane
+    //    per round, so the rounds number the largest per-lane count of marked
+    //    words, not the words.  Survivor order is irrelevant: ranks count
+    //    composites.
     static_assert(EMAX * 4 <= 64, "word mask");
-    uint64_t marks = 0;
+    using Marks = typename std::conditional<EMAX * 4 <= 32, uint32_t, uint64_t>::type;
+    Marks marks = 0;
     const u16x2_t thr_m1 = {(unsigned short)(thr - 1u), (unsigned short)(thr - 1u)};
 #pragma unroll
     for (int e = 0; e < EMAX; ++e)
@@ -865,15 +894,15 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
             const uint32_t k2 = key2[e][w];
             const uint32_t d = __builtin_bit_cast(
                 uint32_t, (u16x2_t)__builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2_t, k2), thr_m1));
-            marks |= (uint64_t)(d != 0u) << (e * 4 + w);
+            marks |= (Marks)(d < 1u ? d : 1u) << (e * 4 + w);
             kw[(e * 4 + w) * kWave + lane] = k2;
         }
     wave_lds_sync();
     uint32_t total = 0;  // wave-uniform
-    while (__ballot(marks != 0ull)) {
-        const bool has = marks != 0ull;
-        const int i = has ? (int)__builtin_ctzll(marks) : 0;
-        marks &= marks - 1ull;
+    while (__ballot(marks != 0)) {
+        const bool has = marks != 0;
+        const int i = has ? (int)__builtin_ctzll((uint64_t)marks) : 0;
+        marks &= marks - 1;
         const uint32_t k2 = kw[i * kWave + lane];
         const uint32_t idx0 = base_idx + (uint32_t)((i >> 2) * kChunk + 2 * (i & 3));
 #pragma unroll
@@ -883,25 +912,17 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
             const uint64_t m = __ballot(sv);
             const uint32_t pos = total + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (sv && pos < kWave) ts.survivors[wave][pos] = (k << 16) | (0xFFFFu - (idx0 + (uint32_t)h));
+            if (sv && pos < kWave)
+                ts.survivors[wave][pos] = (exact_of_prefilter(k) << 16) | (0xFFFFu - (idx0 + (uint32_t)h));
             total += (uint32_t)__popcll(m);
         }
     }
     wave_lds_sync();  // the spill is rewritten by this wave's next tile only
-    if (lane < kTop) out_top[lane] = 0u;
     if (total <= kWave) {
-        // zero padding up to a multiple of 4 (slots past the survivors)
-        if (lane >= (int)total && lane < (int)((total + 3u) & ~3u)) ts.survivors[wave][lane] = 0u;
-        wave_lds_sync();
-        // 4. rank by counting (composites are distinct): rank r -> slot r
-        const uint32_t v = lane < (int)total ? ts.survivors[wave][lane] : 0u;
-        uint32_t rank = 0;
-        for (uint32_t i = 0; i < total; i += 4) {
-            const uint4 w = *reinterpret_cast<const uint4*>(&ts.survivors[wave][i]);
-            rank += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
-        }
-        wave_lds_sync();
-        if (lane < (int)total && rank < (uint32_t)kTop) out_top[rank] = v;
+        // 4. sort the survivors (distinct composites) in registers: lane r
+        //    holds rank r
+        const uint32_t v = wave_sort_desc(lane < (int)total ? ts.survivors[wave][lane] : 0u, lane);
+        if (lane < kTop) out_top[lane] = v;
     } else {
         // many equal values: kTop rounds of "largest composite below the previous"
         uint32_t prev = 0xFFFFFFFFu, mine_top = 0u;
@@ -916,7 +937,9 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
                     uint32_t kw = key2[e][j >> 1];
                     __asm__ volatile("" : "+v"(kw));
                     const uint32_t k = j & 1 ? kw >> 16 : kw & 0xFFFFu;
-                    const uint32_t c = k ? (k << 16) | (0xFFFFu - (base_idx + (uint32_t)(e * kChunk + j))) : 0u;
+                    const uint32_t c = k ? (exact_of_prefilter(k) << 16) |
+                                               (0xFFFFu - (base_idx + (uint32_t)(e * kChunk + j)))
+                                         : 0u;
                     if (c < prev && c > best) best = c;
                 }
             best = wave_max_u32(best);
@@ -1044,23 +1067,13 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     if (lane == 0) ts.flags[wave] = bad;
     __syncthreads();
     uint32_t* part = a.partial_keys + ((int64_t)row * a.tiles + tile) * kTop;
-    // workgroup top-kTop: every wave ranks its kTop entries among all
-    // kWaves * kTop (nonzero composites are distinct; zeros are padding)
-    if (threadIdx.x < kTop) ts.tile_top[threadIdx.x] = 0u;
-    __syncthreads();
-    if (lane < kTop) {
-        const uint32_t v = ts.wave_top[wave * kTop + lane];
-        uint32_t rank = 0;
-#pragma unroll 4
-        for (int i = 0; i < kWaves * kTop; i += 4) {
-            const uint4 w = *reinterpret_cast<const uint4*>(&ts.wave_top[i]);
-            rank += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
-        }
-        if (v != 0u && rank < (uint32_t)kTop) ts.tile_top[rank] = v;
-    }
-    __syncthreads();
+    // workgroup top-kTop: wave 0 sorts the waves' lists in registers, waves
+    // 0-2 first (60 entries), then its top kTop with wave 3's list
     if (wave == 0) {
-        if (lane < kTop) store_device(&part[lane], ts.tile_top[lane]);
+        uint32_t v = wave_sort_desc(lane < 3 * kTop ? ts.wave_top[lane] : 0u, lane);
+        v = lane < kTop ? v : (lane < 2 * kTop ? ts.wave_top[3 * kTop + lane - kTop] : 0u);
+        v = wave_sort_desc(v, lane);
+        if (lane < kTop) store_device(&part[lane], v);
         if (lane == 0)
             store_device(&a.partial_flags[(int64_t)row * a.tiles + tile],
                          ts.flags[0] | ts.flags[1] | ts.flags[2] | ts.flags[3]);

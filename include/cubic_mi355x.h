@@ -199,6 +199,7 @@ CUBIC_API int cubic_root_sample(const void* scores, int scores_fp16, const int64
  *   token_mask   int32 bit words [rows, mask_words] (bit t%32 of word t/32
  *                admits token t) or NULL; needs vocab_start + width <= 32 * mask_words
  *   scores/ids   logits dtype / int64 [rows, candidates], 1 <= candidates <= 64
+ *   1 <= rows <= 65535, 0 <= width <= 2^30
  *   workspace    cubic_greedy_workspace_bytes(rows, width) bytes, zero-filled
  *                once before first use; each launch returns its arrival
  *                counters to zero; one workspace serves launches of the same
