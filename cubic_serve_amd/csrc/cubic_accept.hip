@@ -1068,11 +1068,19 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __syncthreads();
     uint32_t* part = a.partial_keys + ((int64_t)row * a.tiles + tile) * kTop;
     // workgroup top-kTop: wave 0 sorts the waves' lists in registers, waves
-    // 0-2 first (60 entries), then its top kTop with wave 3's list
+    // 0-2 first (60 entries), then its top kTop with wave 3's list (a greedy
+    // row takes the largest of the waves' maxima)
     if (wave == 0) {
-        uint32_t v = wave_sort_desc(lane < 3 * kTop ? ts.wave_top[lane] : 0u, lane);
-        v = lane < kTop ? v : (lane < 2 * kTop ? ts.wave_top[3 * kTop + lane - kTop] : 0u);
-        v = wave_sort_desc(v, lane);
+        uint32_t v;
+        if (greedy_row) {
+            // a greedy tile keeps only slot 0 of each wave's list
+            v = wave_max_u32(lane < kWaves ? ts.wave_top[lane * kTop] : 0u);
+            v = lane == 0 ? v : 0u;
+        } else {
+            v = wave_sort_desc(lane < 3 * kTop ? ts.wave_top[lane] : 0u, lane);
+            v = lane < kTop ? v : (lane < 2 * kTop ? ts.wave_top[3 * kTop + lane - kTop] : 0u);
+            v = wave_sort_desc(v, lane);
+        }
         if (lane < kTop) store_device(&part[lane], v);
         if (lane == 0)
             store_device(&a.partial_flags[(int64_t)row * a.tiles + tile],
