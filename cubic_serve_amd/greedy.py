@@ -43,6 +43,8 @@ class ShardedSamplingParameters:
 
 
 def _require(t: Tensor | None, shape: tuple, dtype: torch.dtype, device: torch.device, label: str):
+    if device.type != "cuda":
+        raise TensorParallelSamplingError(f"{label} must live on a CUDA device")
     if (not isinstance(t, Tensor) or tuple(t.shape) != shape or t.dtype != dtype
             or t.device != device or not t.is_contiguous()):
         raise TensorParallelSamplingError(f"{label} must be a contiguous {dtype} {list(shape)} on {device}")
@@ -91,6 +93,8 @@ def greedy_candidates(logits: Tensor, metadata: Tensor, scores: Tensor, token_id
         raise TensorParallelSamplingError("greedy logits must be bf16/fp16 [rows, V] with unit column stride")
     rows = logits.shape[0]
     width = logits.shape[1] if width is None else width
+    if type(width) is not int or not 0 <= width <= logits.shape[1] or type(vocab_start) is not int or vocab_start < 0:
+        raise TensorParallelSamplingError("greedy visible width or vocabulary start is invalid")
     dev = logits.device
     _require(metadata, (2,), torch.int32, dev, "sampling metadata")
     k = scores.shape[1] if scores.ndim == 2 else 0
