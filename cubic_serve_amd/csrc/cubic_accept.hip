@@ -59,7 +59,7 @@ __device__ __forceinline__ uint32_t order_key16x2(uint32_t w) {
     return (sgn & neg) | (~sgn & pos);
 }
 
-__device__ __forceinline__ uint32_t key16_to_bf16(uint32_t k) {
+__device__ __forceinline__ uint32_t bits_of_key16(uint32_t k) {
     return k >= 0x8000u ? k - 0x8000u : (0x8000u | (0x8000u - k));
 }
 
@@ -822,8 +822,9 @@ __device__ __forceinline__ uint32_t exact_of_prefilter(uint32_t k) {
     return order_key16(raw);
 }
 
-// Returns whether any element of the lane's share is non-finite.
-template <int EMAX>
+// Returns whether any element of the lane's share is non-finite.  HALF:
+// fp16 elements (same sign-magnitude order; non-finite from 0x7C00 up).
+template <int EMAX, bool HALF>
 __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          TileScratch& ts, uint32_t* kw, int lane, int wave, uint32_t* out_top) {
     // 1. prefilter keys, two per word (elements 2w, 2w + 1 of a chunk), 0 =
@@ -844,7 +845,9 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
                 m2 = __builtin_elementwise_max(m2, k);
                 n2 = __builtin_elementwise_min(n2, k);
             }
-        nonfinite = (m2.x >= 0xFF80u) | (m2.y >= 0xFF80u) | (n2.x <= 0x007Fu) | (n2.y <= 0x007Fu);
+        // prefilter keys of inf/NaN: >= 0xFF80 / <= 0x007F (bf16), >= 0xFC00 / <= 0x03FF (fp16)
+        constexpr uint32_t kHi = HALF ? 0xFC00u : 0xFF80u, kLo = HALF ? 0x03FFu : 0x007Fu;
+        nonfinite = (m2.x >= kHi) | (m2.y >= kHi) | (n2.x <= kLo) | (n2.y <= kLo);
     } else {
         const bool partial = chunks * kChunk > width_left;  // wave-uniform
 #pragma unroll
@@ -858,7 +861,7 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
                     valid &= (idx < width_left ? 0x0000FFFFu : 0u) | (idx + 1 < width_left ? 0xFFFF0000u : 0u);
                 }
                 const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
-                const u16x2_t inf = {0x7F80, 0x7F80};
+                const u16x2_t inf = {HALF ? 0x7C00 : 0x7F80, HALF ? 0x7C00 : 0x7F80};
                 nonfinite |= __builtin_bit_cast(uint32_t, (i16x2_t)(mag >= inf)) & valid;
                 key2[e][w] = prefilter_key2(word) & valid;
                 m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2_t, key2[e][w]));
@@ -956,7 +959,7 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
 // composite (value desc, then lowest id; the composite order of tile_top) in
 // out_top[0] and zeros in the other slots.  Returns the non-finite flag as
 // tile_top does.
-template <int EMAX>
+template <int EMAX, bool HALF>
 __device__ bool tile_max(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          int lane, uint32_t* out_top) {
     // Per word (two elements): packed order keys, masked to 0 (empty) past the
@@ -1000,10 +1003,11 @@ __device__ bool tile_max(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
     lane_best = wave_max_u32(lane_best);
     if (lane < kTop) out_top[lane] = lane == 0 ? lane_best : 0u;
     const u16x2_t mm = __builtin_bit_cast(u16x2_t, magmax);
-    return mm.x >= 0x7F80 || mm.y >= 0x7F80;
+    constexpr unsigned short kInf = HALF ? 0x7C00 : 0x7F80;
+    return mm.x >= kInf || mm.y >= kInf;
 }
 
-template <int EMAX, bool FUSED, int SLOTS>
+template <int EMAX, bool FUSED, int SLOTS, bool HALF>
 __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __shared__ TileScratch ts;
     __shared__ VerifyScratch<SLOTS> vs[kWaves];
@@ -1060,8 +1064,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     // row), then the workgroup's top-kTop
     const uint32_t base_idx = (uint32_t)(threadIdx.x * 8);
     const bool nonfinite =
-        greedy_row ? tile_max<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, lane, &ts.wave_top[wave * kTop])
-                   : tile_top<EMAX>(raw, owned ? chunks : 0, base_idx, width_left, ts,
+        greedy_row ? tile_max<EMAX, HALF>(raw, owned ? chunks : 0, base_idx, width_left, lane, &ts.wave_top[wave * kTop])
+                   : tile_top<EMAX, HALF>(raw, owned ? chunks : 0, base_idx, width_left, ts,
                                     &key_spill[wave * EMAX * 4 * kWave], lane, wave, &ts.wave_top[wave * kTop]);
     const uint32_t bad = __any(nonfinite);
     if (lane == 0) ts.flags[wave] = bad;
@@ -1139,7 +1143,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
         }
         const int j = lane;  // capacity <= 64
         if (j < a.capacity) {
-            uint16_t sc = 0x7FC0u;
+            uint16_t sc = HALF ? 0x7E00u : 0x7FC0u;  // quiet NaN padding
             int64_t id = -1;
             if (j < a.count && own) {
                 const bool filled = j < want && my != 0ull;
@@ -1148,7 +1152,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 // except that -0 and +0 share key 0x8000: only then re-read
                 const uint32_t k16 = (uint32_t)(my >> 32);
                 auto exact = [&]() -> uint16_t {
-                    return k16 != 0x8000u ? (uint16_t)key16_to_bf16(k16) : a.logits[(int64_t)r * a.row_stride + gid];
+                    return k16 != 0x8000u ? (uint16_t)bits_of_key16(k16) : a.logits[(int64_t)r * a.row_stride + gid];
                 };
                 if (bad_row) {
                     id = -2;
@@ -1296,10 +1300,17 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
 template <int EMAX, bool FUSED>
 hipError_t launch_accept_slots(const AcceptArgs& a, hipStream_t s) {
     dim3 grid(a.tiles, a.rows), block(kThreads);
-    if (a.block <= 64)
-        accept_kernel<EMAX, FUSED, 1><<<grid, block, 0, s>>>(a);
-    else
-        return hipErrorInvalidValue;
+    if (a.block > 64) return hipErrorInvalidValue;
+    if constexpr (!FUSED) {
+        // fp16 logits: candidate preparation only (the verification takes bf16)
+        if (a.scores_fp16) {
+            accept_kernel<EMAX, false, 1, true><<<grid, block, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    } else {
+        if (a.scores_fp16) return hipErrorInvalidValue;
+    }
+    accept_kernel<EMAX, FUSED, 1, false><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 

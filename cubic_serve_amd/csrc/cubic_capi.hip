@@ -310,7 +310,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
 
 extern "C" {
 
-int cubic_abi_version(void) { return 2; }
+int cubic_abi_version(void) { return 3; }
 
 const char* cubic_last_error(void) { return g_error.c_str(); }
 
@@ -601,11 +601,13 @@ int64_t cubic_candidates_workspace_bytes(int rows, int width) {
     return accept_workspace(rows, rows, width);
 }
 
-int cubic_candidates(const void* logits, int64_t row_stride, int rows, int width,
+int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
                      const float* temperatures, int owned_rows, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream) {
     if (!logits || !temperatures || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "null operand");
+    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16)
+        return fail(CUBIC_EINVAL, "candidate logits dtype must be CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16");
     if (rows <= 0 || width <= 0 || row_stride < width) return fail(CUBIC_EINVAL, "invalid logits geometry");
     if (owned_rows < 0 || owned_rows > rows) return fail(CUBIC_EINVAL, "owned_rows outside 0..rows");
     if (count < 1 || count > kTop || capacity < count || capacity > 64)
@@ -616,6 +618,7 @@ int cubic_candidates(const void* logits, int64_t row_stride, int rows, int width
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "candidate workspace %lld < %lld", (long long)workspace_bytes, (long long)need);
     cubic::AcceptArgs a = {};
     a.logits = (const uint16_t*)logits;
+    a.scores_fp16 = dtype == CUBIC_DTYPE_F16;
     a.row_stride = row_stride;
     a.rows = rows;
     a.width = width;

@@ -17,12 +17,13 @@ constexpr int kGemmWaves = 4;
 constexpr int kMaxGemmMembers = 8;
 
 struct AcceptArgs {
-    const uint16_t* logits;       // [rows, row_stride] bf16
+    const uint16_t* logits;       // [rows, row_stride] bf16 (fp16 when scores_fp16, candidates only)
     int64_t row_stride;           // elements
+    int scores_fp16;
     int rows, width, tiles, tile_width, vector_loads;
     const float* row_temperatures;  // [rows]: 0 = greedy publication
     int owned_rows, count, capacity, all_random;
-    uint16_t* cand_scores;        // [rows, capacity] bf16
+    uint16_t* cand_scores;        // [rows, capacity], the logits' type
     int64_t* cand_ids;            // [rows, capacity]
     int group_rows;               // rows finalised together (1, or depth+1 when fused)
     uint32_t* counters;           // [rows / group_rows], zero between launches

@@ -245,13 +245,15 @@ class LocalCandidatePlan:
 
     One pass over ``local_logits[:active_rows, :visible_width]`` replaces
     torch.topk + candidate_partial + candidate_publish.  TP = 1: vocab_start
-    must be 0 and the local workspace is the gathered one.
+    must be 0 and the local workspace is the gathered one.  Logits and the
+    published scores are bf16 or fp16 (the reference also admits fp32,
+    local_candidates.py:41, which is not admitted here).
     """
 
     def __init__(self, *, local_logits: Tensor, workspace: ShardedSamplingWorkspace,
                  active_rows: int, visible_width: int, local_count: int, vocab_start: int = 0,
                  owned_rows: int | None = None, all_random_rows: bool = False) -> None:
-        if (local_logits.dtype is not torch.bfloat16 or local_logits.ndim != 2
+        if (local_logits.dtype not in (torch.bfloat16, torch.float16) or local_logits.ndim != 2
                 or local_logits.stride(1) != 1
                 or not 0 < active_rows <= local_logits.shape[0]
                 or not 0 < local_count <= visible_width <= local_logits.shape[1]
@@ -288,7 +290,8 @@ class LocalCandidatePlan:
         self.temperatures.copy_(temperatures)
         scores, ids = self.outputs
         with torch.cuda.device(self.logits.device):
-            _native.call("cubic_candidates", self.logits.data_ptr(), self.logits.stride(0),
+            _native.call("cubic_candidates", self.logits.data_ptr(),
+                         int(self.logits.dtype == torch.float16), self.logits.stride(0),
                          self.capacity, self.width, self.temperatures.data_ptr(), self.owned_rows,
                          self.count, scores.shape[1], int(self.all_random), scores.data_ptr(),
                          ids.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),

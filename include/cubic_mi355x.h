@@ -313,14 +313,16 @@ CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_
  * Replaces LocalCandidatePlan.launch (ops/cuda/sampling/local_candidates.py:
  * 206-226: torch.topk + candidate_partial/candidate_publish,
  * local_candidates.cu:19-146) and the greedy argmax (greedy.cu:14-78).
- *   logits        bf16 [rows, row_stride], width <= row_stride visible columns
+ *   logits        [rows, row_stride], width <= row_stride visible columns;
+ *                 dtype CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16 (local_candidates.py:41
+ *                 also admits fp32, which this library does not)
  *   temperatures  f32 [rows]; 0 = greedy row (slot 0 = argmax, lowest id on ties)
- *   scores/ids    bf16 / int64 [rows, capacity]; padding (NaN, -1); rows with a
+ *   scores/ids    logits dtype / int64 [rows, capacity]; padding (NaN, -1); rows with a
  *                 non-finite logit publish id -2 in every counted slot
  *   1 <= count <= 20, count <= capacity <= 64; ties ordered by ascending id.
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_candidates_workspace_bytes(int rows, int width);
-CUBIC_API int cubic_candidates(const void* logits, int64_t row_stride, int rows, int width,
+CUBIC_API int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
                      const float* temperatures, int owned_rows, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream);

@@ -297,11 +297,15 @@ static inline int better(float v, int64_t id, float bv, int64_t bid) {
     return v > bv || (v == bv && id < bid);
 }
 
-EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,
-                             const float* temperatures, int64_t owned_rows, int count,
-                             int capacity, int all_random, uint16_t* out_scores, int64_t* out_ids) {
+/* logits and published scores are bf16 (fp16 = 0) or fp16 (fp16 = 1) bits;
+   the reference publishes its SCORE_TYPE (local_candidates.py:41, :188) */
+EXPORT int oracle_candidates_dtype(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,
+                                   const float* temperatures, int64_t owned_rows, int count,
+                                   int capacity, int all_random, int fp16, uint16_t* out_scores,
+                                   int64_t* out_ids) {
     if (count < 1 || count > capacity || count > 64) return -1;
-    const uint16_t qnan = 0x7fc0u;
+    const uint16_t qnan = fp16 ? 0x7e00u : 0x7fc0u;
+#define ORACLE_SCORE(bits) (fp16 ? oracle_half_to_float(bits) : oracle_bf16_to_float(bits))
     for (int64_t r = 0; r < rows; ++r) {
         uint16_t* sc = out_scores + r * capacity;
         int64_t* id = out_ids + r * capacity;
@@ -310,7 +314,7 @@ EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width
         const uint16_t* row = logits + r * stride;
         int good = 1;
         for (int64_t j = 0; j < width; ++j) {
-            float v = oracle_bf16_to_float(row[j]);
+            float v = ORACLE_SCORE(row[j]);
             if (!isfinite(v)) { good = 0; break; }
         }
         const int greedy = temperatures[r] == 0.0f;
@@ -320,7 +324,7 @@ EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width
         float bv[64]; int64_t bi[64]; uint16_t braw[64]; int filled = 0;
         const int want = count;
         for (int64_t j = 0; j < width; ++j) {
-            float v = oracle_bf16_to_float(row[j]);
+            float v = ORACLE_SCORE(row[j]);
             if (filled == want && !better(v, j, bv[want - 1], bi[want - 1])) continue;
             int pos = filled < want ? filled++ : want - 1;
             while (pos > 0 && better(v, j, bv[pos - 1], bi[pos - 1])) {
@@ -334,7 +338,15 @@ EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width
             sc[0] = braw[0]; id[0] = bi[0];
         }
     }
+#undef ORACLE_SCORE
     return 0;
+}
+
+EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,
+                             const float* temperatures, int64_t owned_rows, int count,
+                             int capacity, int all_random, uint16_t* out_scores, int64_t* out_ids) {
+    return oracle_candidates_dtype(logits, rows, width, stride, temperatures, owned_rows, count,
+                                   capacity, all_random, 0, out_scores, out_ids);
 }
 
 /* ------------------------------------------------------------------------ */

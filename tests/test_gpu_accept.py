@@ -73,6 +73,42 @@ def test_candidates_match_oracle(oracle, rows, width):
         assert np.array_equal(to_bits(scores), want_s)
 
 
+@pytest.mark.parametrize("rows,width", [(3, 300), (4, 32768), (64, 151936), (5, 70001)])
+def test_fp16_candidates_match_oracle(oracle, rows, width):
+    """fp16 logits (local_candidates.py:41): fp16 scores published, fp16 NaN
+    padding, non-finite rows (fp16 inf is 0x7C00) give -2, ties by ascending id."""
+    print(f"fp16 candidates rows={rows} width={width}", flush=True)
+    g = torch.Generator().manual_seed(rows * 11 + width)
+    logits = (torch.randn((rows, width), generator=g) * 3).to(torch.float16)
+    bits = logits.view(torch.int16).numpy().view(np.uint16).copy()
+    bits[0, 5] = bits[0, width - 1] = np.uint16(0x5400)  # 64.0: a tie for the maximum
+    bits[0, 17] = np.uint16(0x8000)
+    bits[0, 18] = np.uint16(0x0000)
+    bits[1, 7] = bits[1, width - 2] = np.uint16(0x5800)  # greedy row: tie across tiles
+    if rows > 2:
+        bits[2, width // 3] = np.uint16(0x7C00)          # +inf row -> id -2
+    if rows > 4:
+        bits[4] = bits[4] | np.uint16(0x8000)             # greedy row, all negative but -0/+0
+        bits[4, 100] = np.uint16(0x8000)
+        bits[4, width - 5] = np.uint16(0x0000)
+    temps = np.array([(0.0 if r % 3 == 1 else 0.7) for r in range(rows)], np.float32)
+    count, capacity = 20, 24
+    scores = torch.empty((rows, capacity), dtype=torch.float16, device=DEV)
+    ids = torch.empty((rows, capacity), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    dev_logits = torch.from_numpy(bits.view(np.int16)).view(torch.float16).to(DEV)
+    plan = sampling.LocalCandidatePlan(local_logits=dev_logits, workspace=ws, active_rows=rows,
+                                       visible_width=width, local_count=count)
+    for _ in range(2):
+        plan.launch(temperatures=torch.from_numpy(temps).to(DEV))
+        torch.cuda.synchronize()
+        want_s, want_i = oracle.candidates(bits, temps, count, capacity, fp16=True)
+        assert np.array_equal(ids.cpu().numpy(), want_i)
+        assert np.array_equal(scores.cpu().view(torch.int16).numpy().view(np.uint16), want_s)
+    if rows > 2:
+        assert (ids[2, :count] == -2).all()
+
+
 def test_candidates_all_equal_row_takes_lowest_ids(oracle):
     rows, width = 2, 40000
     bits = np.full((rows, width), np.uint16(0x3F80), np.uint16)  # all 1.0

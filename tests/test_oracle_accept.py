@@ -93,6 +93,37 @@ def test_candidates_match_brute_force_sort(oracle):
     assert (ids[5, :count] == -2).all()
 
 
+def test_fp16_candidates_match_brute_force_sort(oracle):
+    """fp16 logits (local_candidates.py:41 admits them): same order by value
+    with ascending ids on ties, fp16 scores published unchanged, fp16 NaN padding."""
+    rng = np.random.default_rng(12)
+    rows, width, count = 5, 300, 20
+    values = (np.round(rng.standard_normal((rows, width)) * 4) / 4).astype(np.float16)
+    logits = values.view(np.uint16).copy()
+    logits[2, 17] = np.uint16(0x8000)          # -0.0 ties with +0.0
+    logits[3, 5] = np.uint16(0x0001)           # smallest subnormal
+    temps = np.array([0.7, 0.0, 1.0, 0.5, 1.0], np.float32)
+    logits[4, 200] = np.uint16(0xFC00)         # -inf: non-finite row
+    scores, ids = oracle.candidates(logits, temps, count, capacity=24, fp16=True)
+    f = logits.view(np.float16).astype(np.float64)
+    for r in range(rows):
+        if r == 4:
+            assert (ids[r, :count] == -2).all() and (scores[r] == 0x7E00).all()
+            continue
+        order = sorted(range(width), key=lambda j: (-f[r, j], j))
+        if temps[r] == 0:
+            assert ids[r, 0] == order[0] and scores[r, 0] == logits[r, order[0]]
+            assert (ids[r, 1:] == -1).all() and (scores[r, 1:] == 0x7E00).all()
+        else:
+            assert ids[r, :count].tolist() == order[:count]
+            assert scores[r, :count].tolist() == logits[r, order[:count]].tolist()
+    # the same values as bf16 bits order differently only through rounding:
+    # exact fp16 -> bf16 conversion of quarter-integers keeps the order
+    bf = bf16(values.astype(np.float32))
+    s2, i2 = oracle.candidates(bf[:4], temps[:4], count, capacity=24)
+    assert (i2 == ids[:4]).all()
+
+
 # --------------------------------------------------------------------------- #
 # verify_k1: reference known answers
 # --------------------------------------------------------------------------- #
