@@ -1014,7 +1014,20 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     __shared__ uint32_t key_spill[kWaves * EMAX * 4 * kWave];  // tile_top's key words, word-major
     const int tile = blockIdx.x, row = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const bool owned = row < a.owned_rows;
+    // live sequences and owned rows: host values, or device counts read now
+    int live_rows = a.live_rows, owned_rows = a.owned_rows;
+    if (FUSED && a.live_count) {
+        const int v = a.live_count[0];
+        live_rows = v < 0 ? 0 : (v > a.c ? a.c : v);
+        owned_rows = live_rows * a.group_rows;
+    } else if (!FUSED && a.owned_count) {
+        const int v = a.owned_count[0];
+        owned_rows = v < 0 ? 0 : (v > a.rows ? a.rows : v);
+    }
+    auto row_owned = [&](int r) {
+        return r < owned_rows && (FUSED || !a.row_activity || a.row_activity[r] != 0);
+    };
+    const bool owned = row_owned(row);
     const int64_t begin = (int64_t)tile * a.tile_width;
     const int width_left = (int)((a.width - begin) < a.tile_width ? (a.width - begin) : a.tile_width);
     const int chunks = (width_left + kChunk - 1) / kChunk;
@@ -1097,7 +1110,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     const int row0 = group * a.group_rows;
     for (int gr = wave; gr < a.group_rows; gr += kWaves) {
         const int r = row0 + gr;
-        const bool own = r < a.owned_rows;
+        const bool own = row_owned(r);
         // tiles <= kMaxTiles < 64: one flag per lane; a greedy row's tile
         // maxima (slot 0) are loaded with it, before either is used
         const float temp = a.row_temperatures[r];
@@ -1183,7 +1196,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     auto make_row = [&](int d, bool prefetched) {
         const int64_t pi = (int64_t)d * a.c + c;
         VerifyRow vr;
-        vr.active = c < a.live_rows;
+        vr.active = c < live_rows;
         vr.rows_ok = true;
         const bool in = lane < a.capacity;
         vr.staged = true;
@@ -1282,7 +1295,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
             if (av == 0) { accepted = d; bonus = tok; }
             good = good && (av == 0 || av == 1) && tok >= 0;
         }
-        const bool ok = c < a.live_rows && good;
+        const bool ok = c < live_rows && good;
         a.merged[2 * (int64_t)c] = ok ? accepted : -1;
         a.merged[2 * (int64_t)c + 1] = ok ? bonus : -1;
         if (a.emitted) {

@@ -299,7 +299,8 @@ int accept_scratch(hipStream_t stream, void** out) {
 }
 
 int accept_common(const void* logits, int64_t row_stride, int width, int c, int depth,
-                  int live_rows, const float* row_temperatures, const void* q_scores,
+                  int live_rows, const int32_t* live_count, const float* row_temperatures,
+                  const void* q_scores,
                   const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
                   const float* temperatures, const float* top_ps, const int64_t* top_ks,
                   const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
@@ -310,7 +311,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
 
 extern "C" {
 
-int cubic_abi_version(void) { return 3; }
+int cubic_abi_version(void) { return 4; }
 
 const char* cubic_last_error(void) { return g_error.c_str(); }
 
@@ -602,7 +603,8 @@ int64_t cubic_candidates_workspace_bytes(int rows, int width) {
 }
 
 int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
-                     const float* temperatures, int owned_rows, int count, int capacity,
+                     const float* temperatures, int owned_rows, const int32_t* owned_count,
+                     const uint8_t* row_activity, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream) {
     if (!logits || !temperatures || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "null operand");
@@ -627,6 +629,8 @@ int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows
     a.vector_loads = aligned16(logits) && row_stride % 8 == 0;
     a.row_temperatures = temperatures;
     a.owned_rows = owned_rows;
+    a.owned_count = owned_count;
+    a.row_activity = row_activity;
     a.count = count;
     a.capacity = capacity;
     a.all_random = all_random;
@@ -902,21 +906,23 @@ int64_t cubic_accept_workspace_bytes(int c, int depth, int width) {
 }
 
 int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int depth,
-                 int live_rows, const float* row_temperatures, const void* q_scores,
+                 int live_rows, const int32_t* live_count, const float* row_temperatures,
+                 const void* q_scores,
                  const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
                  const float* temperatures, const float* top_ps, const int64_t* top_ks,
                  const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
                  void* cand_scores, int64_t* cand_ids, int64_t* decisions, int64_t* merged,
                  int64_t* emitted, void* workspace, int64_t workspace_bytes, void* stream) {
     if (!workspace) return fail(CUBIC_EINVAL, "null operand");
-    return accept_common(logits, row_stride, width, c, depth, live_rows, row_temperatures, q_scores,
+    return accept_common(logits, row_stride, width, c, depth, live_rows, live_count, row_temperatures, q_scores,
                          q_ids, capacity, draft_tokens, temperatures, top_ps, top_ks, seeds, ordinals,
                          uniforms, cand_scores, cand_ids, decisions, merged, emitted, workspace,
                          workspace_bytes, stream);
 }
 
 int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int c, int depth,
-                         int live_rows, const float* row_temperatures, const void* q_scores,
+                         int live_rows, const int32_t* live_count, const float* row_temperatures,
+                  const void* q_scores,
                          const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
                          const float* temperatures, const float* top_ps, const int64_t* top_ks,
                          const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
@@ -931,7 +937,7 @@ int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int 
     void* scratch_ptr = nullptr;
     const int rc = accept_scratch((hipStream_t)stream, &scratch_ptr);
     if (rc != CUBIC_OK) return rc;
-    return accept_common(logits, row_stride, width, c, depth, live_rows, row_temperatures, q_scores,
+    return accept_common(logits, row_stride, width, c, depth, live_rows, live_count, row_temperatures, q_scores,
                          q_ids, capacity, draft_tokens, temperatures, top_ps, top_ks, seeds, ordinals,
                          uniforms, cand_scores, cand_ids, decisions, merged, emitted, scratch_ptr,
                          kAcceptScratchBytes, stream);
@@ -942,7 +948,8 @@ int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int 
 namespace {
 
 int accept_common(const void* logits, int64_t row_stride, int width, int c, int depth,
-                  int live_rows, const float* row_temperatures, const void* q_scores,
+                  int live_rows, const int32_t* live_count, const float* row_temperatures,
+                  const void* q_scores,
                   const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
                   const float* temperatures, const float* top_ps, const int64_t* top_ks,
                   const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
@@ -979,6 +986,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
     a.group_rows = depth + 1;
     a.c = c;
     a.live_rows = live_rows;
+    a.live_count = live_count;
     a.block = next_pow2(capacity);
     a.q_scores = (const uint16_t*)q_scores;
     a.q_ids = q_ids;

@@ -23,6 +23,12 @@ struct AcceptArgs {
     int rows, width, tiles, tile_width, vector_loads;
     const float* row_temperatures;  // [rows]: 0 = greedy publication
     int owned_rows, count, capacity, all_random;
+    // device-side counts read when the launch runs (null: the host values):
+    // candidates: rows < owned_count[0] are owned, and row_activity[row] must
+    // be set; fused: sequences < live_count[0] are live (owned rows follow)
+    const int32_t* owned_count;
+    const uint8_t* row_activity;
+    const int32_t* live_count;
     uint16_t* cand_scores;        // [rows, capacity], the logits' type
     int64_t* cand_ids;            // [rows, capacity]
     int group_rows;               // rows finalised together (1, or depth+1 when fused)

@@ -252,7 +252,8 @@ class LocalCandidatePlan:
 
     def __init__(self, *, local_logits: Tensor, workspace: ShardedSamplingWorkspace,
                  active_rows: int, visible_width: int, local_count: int, vocab_start: int = 0,
-                 owned_rows: int | None = None, all_random_rows: bool = False) -> None:
+                 owned_rows: int | None = None, all_random_rows: bool = False,
+                 row_activity: Tensor | None = None, metadata: Tensor | None = None) -> None:
         if (local_logits.dtype not in (torch.bfloat16, torch.float16) or local_logits.ndim != 2
                 or local_logits.stride(1) != 1
                 or not 0 < active_rows <= local_logits.shape[0]
@@ -271,6 +272,19 @@ class LocalCandidatePlan:
             raise ValueError("candidate count must be <= 20 and capacity <= 64")
         if local_logits.device.type != "cuda":
             raise ValueError("local candidate preparation requires one CUDA device")
+        # replay-time ownership (local_candidates.py:55-70): rows below the
+        # device count metadata[0] whose activity flag is set
+        if row_activity is not None and (row_activity.dtype != torch.bool
+                                         or row_activity.shape != (active_rows,)
+                                         or row_activity.device != local_logits.device
+                                         or not row_activity.is_contiguous()):
+            raise ValueError("local candidate row activity has an invalid tensor ABI")
+        if metadata is not None and (metadata.dtype != torch.int32 or metadata.ndim != 1
+                                     or metadata.numel() < 1
+                                     or metadata.device != local_logits.device
+                                     or not metadata.is_contiguous()):
+            raise ValueError("local candidate metadata has an invalid tensor ABI")
+        self.row_activity, self.metadata = row_activity, metadata
         self.logits, self.capacity = local_logits, active_rows
         self.width, self.count = visible_width, local_count
         self.outputs = (workspace.local_scores, workspace.local_token_ids)
@@ -293,6 +307,7 @@ class LocalCandidatePlan:
             _native.call("cubic_candidates", self.logits.data_ptr(),
                          int(self.logits.dtype == torch.float16), self.logits.stride(0),
                          self.capacity, self.width, self.temperatures.data_ptr(), self.owned_rows,
+                         _native.ptr(self.metadata), _native.ptr(self.row_activity),
                          self.count, scores.shape[1], int(self.all_random), scores.data_ptr(),
                          ids.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),
                          _native.stream_of(self.logits.device))
@@ -351,12 +366,22 @@ class MTPVerifyPlan:
             raise ValueError("vocabulary width not admitted")
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
 
-    def launch(self, live_rows: int | None = None) -> None:
-        live = self.c if live_rows is None else live_rows
+    def launch(self, live_rows: int | Tensor | None = None) -> None:
+        """``live_rows``: live sequences, a host int or a device int32 tensor
+        whose first element is read when the launch runs (the reference's
+        ``ctx``; a captured launch then follows later writes to it)."""
+        live, live_ptr = self.c, None
+        if isinstance(live_rows, Tensor):
+            if (live_rows.dtype != torch.int32 or live_rows.device != self.logits.device
+                    or live_rows.numel() < 1 or not live_rows.is_contiguous()):
+                raise ValueError("live row count must be a device int32 tensor")
+            live_ptr = live_rows.data_ptr()
+        elif live_rows is not None:
+            live = live_rows
         d, t, p, k_, s, o = self.params
         with torch.cuda.device(self.logits.device):
             _native.call("cubic_accept", self.logits.data_ptr(), self.logits.stride(0), self.width,
-                         self.c, self.depth, live, self.row_temperatures.data_ptr(),
+                         self.c, self.depth, live, live_ptr, self.row_temperatures.data_ptr(),
                          self.q_scores.data_ptr(), self.q_token_ids.data_ptr(), self.k,
                          d.data_ptr(), t.data_ptr(), p.data_ptr(), k_.data_ptr(), s.data_ptr(),
                          o.data_ptr(), _native.ptr(self.uniforms),

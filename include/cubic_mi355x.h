@@ -319,11 +319,16 @@ CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_
  *   temperatures  f32 [rows]; 0 = greedy row (slot 0 = argmax, lowest id on ties)
  *   scores/ids    logits dtype / int64 [rows, capacity]; padding (NaN, -1); rows with a
  *                 non-finite logit publish id -2 in every counted slot
+ *   owned rows: row < owned_rows, or row < owned_count[0] when owned_count
+ *                 (device int32, the reference's metadata) is given, read when
+ *                 the launch runs; and row_activity[row] != 0 when that bool
+ *                 [rows] array is given.  Other rows publish padding only.
  *   1 <= count <= 20, count <= capacity <= 64; ties ordered by ascending id.
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_candidates_workspace_bytes(int rows, int width);
 CUBIC_API int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
-                     const float* temperatures, int owned_rows, int count, int capacity,
+                     const float* temperatures, int owned_rows, const int32_t* owned_count,
+                     const uint8_t* row_activity, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
@@ -362,6 +367,10 @@ CUBIC_API int cubic_merge_prefix(const int64_t* decisions, int c, int depth, con
  * merge_prefix in finish_review (executor/draft_graph.py:1034-1067), in one
  * launch and one pass over the logits.  TP = 1.
  *   logits            bf16 [c*(depth+1), row_stride], row c*(depth+1)+d
+ *   live sequences    c' < live_rows, or c' < live_count[0] when live_count
+ *                     (device int32, the reference's ctx[0]) is given, read
+ *                     when the launch runs; other sequences publish padding
+ *                     and (-1, -1) decisions
  *   row_temperatures  f32 [c*(depth+1)] candidate publication temperatures
  *   q_scores/q_ids    bf16/int64 [depth, c, capacity] draft candidates
  *   draft_tokens, top_ks, seeds, ordinals  int64 [depth, c];
@@ -373,7 +382,8 @@ CUBIC_API int cubic_merge_prefix(const int64_t* decisions, int c, int depth, con
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_accept_workspace_bytes(int c, int depth, int width);
 CUBIC_API int cubic_accept(const void* logits, int64_t row_stride, int width, int c, int depth,
-                 int live_rows, const float* row_temperatures, const void* q_scores,
+                 int live_rows, const int32_t* live_count, const float* row_temperatures,
+                 const void* q_scores,
                  const int64_t* q_ids, int capacity, const int64_t* draft_tokens,
                  const float* temperatures, const float* top_ps, const int64_t* top_ks,
                  const int64_t* seeds, const int64_t* ordinals, const float* uniforms,
@@ -394,7 +404,8 @@ CUBIC_API int cubic_accept(const void* logits, int64_t row_stride, int width, in
  * (launches on concurrent streams) race and must be ordered by the caller.
  * ------------------------------------------------------------------------- */
 CUBIC_API int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int c,
-                                   int depth, int live_rows, const float* row_temperatures,
+                                   int depth, int live_rows, const int32_t* live_count,
+                                   const float* row_temperatures,
                                    const void* q_scores, const int64_t* q_ids, int capacity,
                                    const int64_t* draft_tokens, const float* temperatures,
                                    const float* top_ps, const int64_t* top_ks,

@@ -231,7 +231,8 @@ def test_merge_prefix_matches_oracle(oracle):
 # --------------------------------------------------------------------------- #
 # fused verify from logits
 # --------------------------------------------------------------------------- #
-def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, live=None, k=20):
+def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, live=None, k=20,
+                device_live=False):
     rng = np.random.default_rng(seed)
     g = torch.Generator().manual_seed(seed)
     rows = c * (depth + 1)
@@ -287,6 +288,26 @@ def _fused_case(oracle, c, depth, width, stochastic, seed, use_uniforms=True, li
         else:
             assert emitted[s, :acc].tolist() == drafts[:acc, s].tolist()
             assert emitted[s, acc] == bonus and (emitted[s, acc + 1:] == -1).all()
+    if device_live:
+        # one captured launch reading the live count on the device, replayed
+        # for several counts (eager work between replays)
+        count = torch.tensor([c], dtype=torch.int32, device=DEV)
+        plan.launch(live_rows=count)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            plan.launch(live_rows=count)
+        for n in (c, live, 1, 0, c - 1):
+            count.fill_(n)
+            graph.replay()
+            torch.cuda.synchronize()
+            w = oracle.verify_from_logits(tbits, q_scores, q_ids, drafts, temps, top_ps, top_ks, seeds,
+                                          ordinals, n, uniforms, count=k)
+            assert np.array_equal(plan.candidate_ids.cpu().numpy(), w[1]), n
+            assert np.array_equal(to_bits(plan.candidate_scores), w[0]), n
+            assert np.array_equal(plan.decisions.cpu().numpy(), w[2]), n
+            assert np.array_equal(plan.merged.cpu().numpy(), w[3]), n
+        graph.reset()
     return want
 
 
@@ -327,3 +348,47 @@ def test_fused_deep_drafts(oracle, stochastic):
     """k = 5 drafts: depths past the fourth are verified on a second pass of
     the waves, reading their inputs directly rather than from the prefetch."""
     _fused_case(oracle, 3, 5, 5000, stochastic, 13, live=2)
+
+
+@pytest.mark.parametrize("stochastic", [True, False])
+def test_fused_device_live_count_in_one_graph(oracle, stochastic):
+    """The live count read on the device when the launch runs (the reference
+    composition writes ctx[0] into the sampler metadata, draft_graph.py:
+    1046-1067): one captured launch serves every count."""
+    _fused_case(oracle, 8, 2, 9000, stochastic, 41, live=5, device_live=True)
+
+
+def test_candidates_device_metadata_and_activity(oracle):
+    """LocalCandidatePlan(metadata=, row_activity=) (local_candidates.py:55-70):
+    rows below metadata[0] whose activity flag is set are owned, read at replay."""
+    rows, width, count = 8, 20000, 20
+    g = torch.Generator().manual_seed(77)
+    bits = to_bits((torch.randn((rows, width), generator=g) * 3).to(torch.bfloat16)).copy()
+    temps = np.array([0.0, 0.7] * (rows // 2), np.float32)
+    scores = torch.empty((rows, count), dtype=torch.bfloat16, device=DEV)
+    ids = torch.empty((rows, count), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    meta = torch.tensor([rows, 0], dtype=torch.int32, device=DEV)
+    activity = torch.ones(rows, dtype=torch.bool, device=DEV)
+    plan = sampling.LocalCandidatePlan(local_logits=from_bits(bits), workspace=ws, active_rows=rows,
+                                       visible_width=width, local_count=count, metadata=meta,
+                                       row_activity=activity)
+    full_s, full_i = oracle.candidates(bits, temps, count, count)
+    t_dev = torch.from_numpy(temps).to(DEV)
+    plan.launch(temperatures=t_dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.launch(temperatures=t_dev)
+    for n, act in ((rows, [1] * rows), (5, [1, 0, 1, 1, 0, 1, 1, 1]), (0, [1] * rows), (3, [0] * rows)):
+        meta[0] = n
+        activity.copy_(torch.tensor(act, dtype=torch.bool))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_s, got_i = to_bits(scores), ids.cpu().numpy()
+        for r in range(rows):
+            if r < n and act[r]:
+                assert np.array_equal(got_i[r], full_i[r]) and np.array_equal(got_s[r], full_s[r]), (n, r)
+            else:
+                assert (got_i[r] == -1).all() and (got_s[r] == NAN_BF16).all(), (n, r)
+    graph.reset()

@@ -54,7 +54,7 @@ def _run_both(c, depth, width, k, temperature, seed):
         t.fill_(-7)
     with torch.cuda.device(DEV):
         _native.call("cubic_accept_noalloc", plan.logits.data_ptr(), plan.logits.stride(0),
-                     plan.width, c, depth, c, plan.row_temperatures.data_ptr(),
+                     plan.width, c, depth, c, None, plan.row_temperatures.data_ptr(),
                      plan.q_scores.data_ptr(), plan.q_token_ids.data_ptr(), k,
                      dev["draft_tokens"].data_ptr(), dev["temperatures"].data_ptr(),
                      dev["top_ps"].data_ptr(), dev["top_ks"].data_ptr(), dev["seeds"].data_ptr(),
@@ -84,6 +84,6 @@ def test_noalloc_rejects_plans_beyond_the_static_scratch():
     c, depth, width = 4096, 8, 400003
     need = lib.cubic_accept_workspace_bytes(c, depth, width)
     assert need > (4 << 20)
-    rc = lib.cubic_accept_noalloc(*([0] * 2), width, c, depth, c, *([0] * 3), 20, *([0] * 13))
+    rc = lib.cubic_accept_noalloc(*([0] * 2), width, c, depth, c, *([0] * 4), 20, *([0] * 13))
     assert rc == -4
     assert b"static scratch" in lib.cubic_last_error()
