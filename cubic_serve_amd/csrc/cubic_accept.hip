@@ -13,7 +13,9 @@
 // candidate preparation, the k+1 rows of one sequence for the fused verify)
 // merges the tiles, publishes the candidates and, in fused mode, verifies
 // every depth and merges the prefix.  Arrival counters live in the caller's
-// workspace; the finishing workgroup returns its counter to zero.
+// workspace; the finishing workgroup returns its counter to zero.  Candidate
+// preparation also takes fp16 logits; the live and owned row counts may be
+// device values read when the launch runs (one captured graph, any count).
 //
 // Wave-level reductions follow fixed orders (butterfly sums in ascending
 // lane distance, row-wise scans; cubic_device.h) that the CPU restatement
@@ -37,9 +39,10 @@ constexpr int kChunk = kThreads * 8;  // elements per 16-byte load round
 constexpr int64_t kInt64Max = 0x7FFFFFFFFFFFFFFFLL;
 
 // --------------------------------------------------------------------------
-// Ordering keys.  key16 maps bf16 bits to an unsigned order that compares like
-// the float values and treats -0 and +0 as equal; the low 16 bits hold
-// 0xFFFF - local index so that the larger composite is the lower id on ties.
+// Ordering keys.  key16 maps sign-magnitude 16-bit floats (bf16 and fp16
+// alike) to an unsigned order that compares like the values and treats -0
+// and +0 as equal; the low 16 bits hold 0xFFFF - local index so that the
+// larger composite is the lower id on ties.
 // --------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t order_key16(uint32_t u) {
     const uint32_t m = u & 0x7FFFu;
@@ -63,7 +66,6 @@ __device__ __forceinline__ uint32_t bits_of_key16(uint32_t k) {
     return k >= 0x8000u ? k - 0x8000u : (0x8000u | (0x8000u - k));
 }
 
-__device__ __forceinline__ bool nonfinite_bf16(uint32_t u) { return (u & 0x7F80u) == 0x7F80u; }
 
 __device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
     const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
