@@ -40,7 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_moe_route": (I32, [P, I32, P, P, I32, I32, I32, P, P, P, P, I32, P]),
     "cubic_moe_compact": (I32, [P, I32, I32, I32, I32, P, P, P, P, P, P]),
     "cubic_candidates_workspace_bytes": (I64, [I32, I32]),
-    "cubic_candidates": (I32, [P, I32, I64, I32, I32, P, I32, P, P, I32, I32, I32, P, P, P, I64, P]),
+    "cubic_candidates": (I32, [P, I32, I64, I32, I32, I64, P, I32, P, P, I32, I32, I32, P, P, P, I64, P]),
     "cubic_verify_candidates": (I32, [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32,
                                       I32, I32, P, P]),
     "cubic_root_sample": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P, P]),

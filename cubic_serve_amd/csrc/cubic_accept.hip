@@ -1172,10 +1172,10 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
                 if (bad_row) {
                     id = -2;
                 } else if (!greedy_pub) {
-                    if (filled) { sc = exact(); id = gid; }
+                    if (filled) { sc = exact(); id = gid + a.vocab_start; }
                 } else if (!a.all_random && j == 0 && filled) {
                     sc = exact();
-                    id = gid;
+                    id = gid + a.vocab_start;
                 }
             }
             a.cand_scores[(int64_t)r * a.capacity + j] = sc;

@@ -311,7 +311,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
 
 extern "C" {
 
-int cubic_abi_version(void) { return 4; }
+int cubic_abi_version(void) { return 5; }
 
 const char* cubic_last_error(void) { return g_error.c_str(); }
 
@@ -603,13 +603,14 @@ int64_t cubic_candidates_workspace_bytes(int rows, int width) {
 }
 
 int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
-                     const float* temperatures, int owned_rows, const int32_t* owned_count,
+                     int64_t vocab_start, const float* temperatures, int owned_rows, const int32_t* owned_count,
                      const uint8_t* row_activity, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream) {
     if (!logits || !temperatures || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "null operand");
     if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16)
         return fail(CUBIC_EINVAL, "candidate logits dtype must be CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16");
+    if (vocab_start < 0) return fail(CUBIC_EINVAL, "negative vocabulary start");
     if (rows <= 0 || width <= 0 || row_stride < width) return fail(CUBIC_EINVAL, "invalid logits geometry");
     if (owned_rows < 0 || owned_rows > rows) return fail(CUBIC_EINVAL, "owned_rows outside 0..rows");
     if (count < 1 || count > kTop || capacity < count || capacity > 64)
@@ -631,6 +632,7 @@ int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows
     a.owned_rows = owned_rows;
     a.owned_count = owned_count;
     a.row_activity = row_activity;
+    a.vocab_start = vocab_start;
     a.count = count;
     a.capacity = capacity;
     a.all_random = all_random;

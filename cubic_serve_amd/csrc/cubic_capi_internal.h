@@ -23,6 +23,7 @@ struct AcceptArgs {
     int rows, width, tiles, tile_width, vector_loads;
     const float* row_temperatures;  // [rows]: 0 = greedy publication
     int owned_rows, count, capacity, all_random;
+    int64_t vocab_start;          // published ids: vocab_start + column (candidates only)
     // device-side counts read when the launch runs (null: the host values):
     // candidates: rows < owned_count[0] are owned, and row_activity[row] must
     // be set; fused: sequences < live_count[0] are live (owned rows follow)

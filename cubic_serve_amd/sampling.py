@@ -244,8 +244,8 @@ class LocalCandidatePlan:
     """Vocab logits -> published top-k candidates, bound before capture.
 
     One pass over ``local_logits[:active_rows, :visible_width]`` replaces
-    torch.topk + candidate_partial + candidate_publish.  TP = 1: vocab_start
-    must be 0 and the local workspace is the gathered one.  Logits and the
+    torch.topk + candidate_partial + candidate_publish over this rank's
+    vocabulary shard; published ids are ``vocab_start`` + column.  Logits and the
     published scores are bf16 or fp16 (the reference also admits fp32,
     local_candidates.py:41, which is not admitted here).
     """
@@ -266,8 +266,9 @@ class LocalCandidatePlan:
                 or not workspace.local_scores.is_contiguous()
                 or not workspace.local_token_ids.is_contiguous()):
             raise ValueError("local candidate preparation has an invalid tensor ABI")
-        if vocab_start != 0:
-            raise ValueError("single-GPU candidate preparation owns the whole vocabulary")
+        if type(vocab_start) is not int or vocab_start < 0:
+            raise ValueError("vocabulary start must be a non-negative int")
+        self.vocab_start = vocab_start
         if local_count > 20 or workspace.local_scores.shape[1] > 64:
             raise ValueError("candidate count must be <= 20 and capacity <= 64")
         if local_logits.device.type != "cuda":
@@ -306,7 +307,8 @@ class LocalCandidatePlan:
         with torch.cuda.device(self.logits.device):
             _native.call("cubic_candidates", self.logits.data_ptr(),
                          int(self.logits.dtype == torch.float16), self.logits.stride(0),
-                         self.capacity, self.width, self.temperatures.data_ptr(), self.owned_rows,
+                         self.capacity, self.width, self.vocab_start, self.temperatures.data_ptr(),
+                         self.owned_rows,
                          _native.ptr(self.metadata), _native.ptr(self.row_activity),
                          self.count, scores.shape[1], int(self.all_random), scores.data_ptr(),
                          ids.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),

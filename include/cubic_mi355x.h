@@ -317,6 +317,7 @@ CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_
  *                 dtype CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16 (local_candidates.py:41
  *                 also admits fp32, which this library does not)
  *   temperatures  f32 [rows]; 0 = greedy row (slot 0 = argmax, lowest id on ties)
+ *   vocab_start   first token of this shard: published ids are vocab_start + column
  *   scores/ids    logits dtype / int64 [rows, capacity]; padding (NaN, -1); rows with a
  *                 non-finite logit publish id -2 in every counted slot
  *   owned rows: row < owned_rows, or row < owned_count[0] when owned_count
@@ -327,7 +328,7 @@ CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_
  * ------------------------------------------------------------------------- */
 CUBIC_API int64_t cubic_candidates_workspace_bytes(int rows, int width);
 CUBIC_API int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
-                     const float* temperatures, int owned_rows, const int32_t* owned_count,
+                     int64_t vocab_start, const float* temperatures, int owned_rows, const int32_t* owned_count,
                      const uint8_t* row_activity, int count, int capacity,
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream);

@@ -263,8 +263,10 @@ def check_linear_enclosure(x_bits: np.ndarray, w_bits: np.ndarray, y_bits: np.nd
 # A13-A15: acceptance
 # --------------------------------------------------------------------------- #
 def candidates(logits_bits: np.ndarray, temperatures: np.ndarray, count: int, capacity: int | None = None,
-               owned_rows: int | None = None, all_random: bool = False, fp16: bool = False):
-    """[M, V] bf16 (or fp16) logits -> ([M, capacity] scores of the same type, [M, capacity] int64 ids)."""
+               owned_rows: int | None = None, all_random: bool = False, fp16: bool = False,
+               vocab_start: int = 0):
+    """[M, V] bf16 (or fp16) logits -> ([M, capacity] scores of the same type, [M, capacity] int64 ids);
+    real ids are vocab_start + column (candidate_publish adds the shard's start)."""
     logits_bits = _c(logits_bits, np.uint16)
     rows, width = logits_bits.shape
     capacity = count if capacity is None else capacity
@@ -279,6 +281,7 @@ def candidates(logits_bits: np.ndarray, temperatures: np.ndarray, count: int, ca
                                        _p(scores), _p(ids))
     if rc:
         raise ValueError("invalid candidate count")
+    ids[ids >= 0] += vocab_start
     return scores, ids
 
 

@@ -23,7 +23,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.SIGNATURES), "ctypes signatures drift from the header"
-    assert lib.cubic_abi_version() == 4
+    assert lib.cubic_abi_version() == 5
 
 
 def test_host_planning_entry_points():
@@ -43,9 +43,9 @@ def test_host_planning_entry_points():
 
 def test_invalid_arguments_fail_before_any_launch():
     with pytest.raises(ValueError, match="count"):
-        _native.call("cubic_candidates", 16, 0, 100, 2, 100, 16, 2, None, None, 21, 21, 0, 16, 16, 16, 1 << 20, None)
+        _native.call("cubic_candidates", 16, 0, 100, 2, 100, 0, 16, 2, None, None, 21, 21, 0, 16, 16, 16, 1 << 20, None)
     with pytest.raises(ValueError, match="dtype"):
-        _native.call("cubic_candidates", 16, 2, 100, 2, 100, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 20, None)
+        _native.call("cubic_candidates", 16, 2, 100, 2, 100, 0, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 20, None)
     with pytest.raises(ValueError, match="tp"):
         _native.call("cubic_verify_candidates", *([16] * 13), 0, 9, 4, 8, 20, 4, 16, None)
     with pytest.raises(ValueError, match="group_in"):

@@ -392,3 +392,24 @@ def test_candidates_device_metadata_and_activity(oracle):
             else:
                 assert (got_i[r] == -1).all() and (got_s[r] == NAN_BF16).all(), (n, r)
     graph.reset()
+
+
+def test_candidates_vocab_shard_offset(oracle):
+    """A rank's vocabulary shard: published ids are vocab_start + column
+    (LocalCandidatePlan(vocab_start=...), local_candidates.py:25-40)."""
+    rows, width, count, start = 3, 5000, 20, 151936 - 5000
+    g = torch.Generator().manual_seed(5)
+    bits = to_bits((torch.randn((rows, width), generator=g) * 3).to(torch.bfloat16)).copy()
+    bits[2, 77] = np.uint16(0x7FC0)
+    temps = np.array([0.7, 0.0, 0.7], np.float32)
+    scores = torch.empty((rows, count), dtype=torch.bfloat16, device=DEV)
+    ids = torch.empty((rows, count), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    plan = sampling.LocalCandidatePlan(local_logits=from_bits(bits), workspace=ws, active_rows=rows,
+                                       visible_width=width, local_count=count, vocab_start=start)
+    plan.launch(temperatures=torch.from_numpy(temps).to(DEV))
+    torch.cuda.synchronize()
+    want_s, want_i = oracle.candidates(bits, temps, count, count, vocab_start=start)
+    assert np.array_equal(ids.cpu().numpy(), want_i)
+    assert np.array_equal(to_bits(scores), want_s)
+    assert ids[0].min().item() >= start and (ids[2, :count] == -2).all()
