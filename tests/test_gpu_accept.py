@@ -413,3 +413,44 @@ def test_candidates_vocab_shard_offset(oracle):
     assert np.array_equal(ids.cpu().numpy(), want_i)
     assert np.array_equal(to_bits(scores), want_s)
     assert ids[0].min().item() >= start and (ids[2, :count] == -2).all()
+
+
+@pytest.mark.parametrize("use_uniforms", [True, False])
+def test_speculative_output_follows_the_target_distribution(use_uniforms):
+    """Speculative sampling leaves the target distribution unchanged
+    (tests/generation/test_tp_sampling.py:199-216): drafts drawn from q
+    (0.7 / 0.3), target 0.2 / 0.8; the emitted token -- the draft when
+    accepted, the residual sample otherwise -- over 20000 independent rows
+    follows the target.  top_k = 2: a row admits exactly its two real
+    candidates.  With Philox draws (distinct seeds) this also checks the
+    on-device generator."""
+    n, k = 20000, 20
+    rng = np.random.default_rng(4301)
+    q_bits = np.full((1, n, k), NAN_BF16, np.uint16)
+    p_bits = np.full((1, 2, k), NAN_BF16, np.uint16)
+    q_ids = np.full((1, n, k), -1, np.int64)
+    p_ids = np.full((1, 2, k), -1, np.int64)
+    q_bits[0, :, :2] = bf16(np.log([0.7, 0.3]))
+    p_bits[0, :, :2] = bf16(np.log([0.2, 0.8]))
+    q_ids[0, :, :2] = [0, 1]
+    p_ids[0, :, :2] = [0, 1]
+
+    def softmax(bits):
+        v = (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        e = np.exp(v - v.max())
+        return e / e.sum()
+
+    q_probs, target = softmax(q_bits[0, 0, :2]), softmax(p_bits[0, 0, :2])
+    drafts = (rng.random(n) >= q_probs[0]).astype(np.int64)
+    uniforms = rng.random((n, 2)).astype(np.float32) if use_uniforms else None
+    seeds = rng.integers(0, 2**40, n).astype(np.int64)
+    ordinals = rng.integers(0, 2**20, n).astype(np.int64)
+    dec = _verify(q_bits, q_ids, p_bits, p_ids, np.zeros(n, np.int32), drafts,
+                  np.ones(n, np.float32), np.ones(n, np.float32), np.full(n, 2, np.int64),
+                  seeds, ordinals, n, uniforms=uniforms)
+    assert (dec[:, 0] >= 0).all()
+    emitted = np.where(dec[:, 0] == 1, drafts, dec[:, 1])
+    observed = np.bincount(emitted, minlength=2)[:2] / n
+    assert np.abs(observed - target).max() < 0.02, (observed, target)
+    # and the drafts alone follow q, not the target (the test is not vacuous)
+    assert abs(drafts.mean() - q_probs[1]) < 0.02 and abs(q_probs[1] - target[1]) > 0.4
