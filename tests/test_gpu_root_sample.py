@@ -186,3 +186,40 @@ def test_graph_replay_reads_new_operands(oracle):
         want_t, want_v = oracle_of(oracle, ops)
         assert np.array_equal(ops[7].cpu().numpy(), want_t), i
         assert np.array_equal(ops[8].cpu().numpy(), want_v), i
+
+
+def test_sampled_tokens_follow_the_truncated_softmax():
+    """20000 rows of the same gathered candidates, distinct (seed, ordinal):
+    the Philox-driven draws follow softmax(score / T) restricted to the top-k
+    and renormalised over the top-p prefix (exclusive CDF <= top_p), within
+    0.015 per token, and never leave that support."""
+    rows, tp, k = 20000, 2, 4
+    vals = np.array([[2.0, 1.5, 1.0, 0.5], [1.75, 1.25, 0.75, 0.25]], np.float32)  # bf16-exact
+    scores = torch.from_numpy(vals).view(tp, 1, k).expand(tp, rows, k).to(torch.bfloat16).contiguous().to(DEV)
+    ids = torch.arange(tp * k, device=DEV, dtype=torch.int64).view(tp, 1, k).expand(tp, rows, k).contiguous()
+    temp, top_p, top_k = 0.8, 0.85, 4  # top_k <= K, the candidates per rank
+    g = torch.Generator().manual_seed(99)
+    ops = [scores, ids, torch.full((rows,), temp, device=DEV), torch.full((rows,), top_p, device=DEV),
+           torch.full((rows,), top_k, dtype=torch.int64, device=DEV),
+           torch.randint(0, 2**40, (rows,), generator=g).to(DEV),
+           torch.randint(0, 2**30, (rows,), generator=g).to(DEV),
+           torch.empty(rows, dtype=torch.int64, device=DEV), torch.empty(rows, dtype=torch.bool, device=DEV)]
+    prim = sampling.RootTopKTopPSamplingPrimitive(*ops)
+    prim.launch(*ops)
+    torch.cuda.synchronize()
+    assert bool(ops[8].all())
+    # expected: global order by value, top_k, softmax at T, exclusive-CDF top-p
+    flat = [(float(vals[r, c]), r * k + c) for r in range(tp) for c in range(k)]
+    flat.sort(key=lambda t: (-t[0], t[1]))
+    kept = flat[:top_k]
+    w = np.exp((np.array([v for v, _ in kept]) - kept[0][0]) / temp)
+    p = w / w.sum()
+    excl = np.concatenate([[0.0], np.cumsum(p)[:-1]])
+    p = np.where(excl <= top_p, p, 0.0)
+    p = p / p.sum()
+    expected = np.zeros(tp * k)
+    for (v, tok), pr in zip(kept, p):
+        expected[tok] = pr
+    observed = np.bincount(ops[7].cpu().numpy(), minlength=tp * k) / rows
+    assert np.abs(observed - expected).max() < 0.015, (observed, expected)
+    assert observed[expected == 0].sum() == 0
