@@ -16,6 +16,8 @@ P = ctypes.c_void_p
 I32 = ctypes.c_int
 I64 = ctypes.c_int64
 
+ABI_VERSION = 5  # cubic_abi_version() of the library these signatures describe
+
 # name -> (restype, argtypes); mirrors include/cubic_mi355x.h
 SIGNATURES: dict[str, tuple] = {
     "cubic_abi_version": (I32, []),
@@ -84,6 +86,9 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        if handle.cubic_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{_LIB_PATH} implements ABI {handle.cubic_abi_version()}, these "
+                               f"bindings expect {ABI_VERSION}: rebuild the library")
         _lib = handle
     return _lib
 

@@ -36,6 +36,10 @@ extern "C" {
 #define CUBIC_FMT_I8_SCALE_I4_AB 1    /* "int8-scale-int4-ab-global-fp32" */
 #define CUBIC_FMT_E5M9_CURVE2 2       /* "e5m9-scale-curve2-tensor-fp16" */
 
+/* ABI revision, raised whenever an entry point's arguments change: 2 added
+ * the GEMM dtype, 3 the candidate dtype, 4 the device live/owned counts of
+ * cubic_accept(_noalloc) and cubic_candidates, 5 the candidate vocab_start.
+ * This header describes revision 5. */
 CUBIC_API int cubic_abi_version(void);
 CUBIC_API const char* cubic_last_error(void);
 
