@@ -621,10 +621,13 @@ void gemm_kernel(GemmArgs a) {
 // Small-row GEMM (M <= 4; bits <= 4; groups of whole k-blocks)
 //   grid.x: 16-column tiles; a workgroup of G waves owns one tile and all of K.
 //   Wave w streams the tile's k-blocks [w * kbw, (w + 1) * kbw) in chunks of
-//   D: codes, the group's level table and the activation fragments of every
-//   row (rows past M re-read row M-1; their outputs are never stored), all
-//   loaded straight into registers -- no LDS staging and no barrier in the
-//   loop.  The MFMA sums each 32-k fragment; the G per-wave
+//   D: codes, the group's level table and the k-block's 4 x 128 activations
+//   (one 16-byte load per lane; rows past M read zero), all loaded straight
+//   into registers -- no LDS staging and no barrier in the loop.  The MFMA
+//   A fragments are gathered across lanes with ds_bpermute: the loop is
+//   bound by vector-memory instructions issued, and the four per-fragment
+//   activation loads it replaces cost as much of that path as 4 KB of codes
+//   while carrying at most 1 KB.  The MFMA sums each 32-k fragment; the G per-wave
 //   partial sums are added in wave order through LDS at the end, so the K
 //   partition depends on K alone (not on M or on grouping).
 // (quantization/common/small_rows.cu:94-241 and small_rows_cost.py:438-501
@@ -658,15 +661,27 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.x), 0, (int)((int64_t)a.m * a.ldx * 2), 0x00020000);
     const int gpk = a.group_in / kKBlock;  // k-blocks per metadata group
-    const int x_lane = col < a.m ? (int)((int64_t)col * a.ldx * 2) + 64 * q : kOut;
+    // Activations: one 16-byte load per lane and k-block covers the 4 x 128
+    // block (lane l: row l / 16, elements 8 (l % 16) .. + 7); the MFMA
+    // A fragments are gathered from it across lanes.  Rows past M read zero.
+    const int x_row = lane >> 4, x_chunk = lane & 15;
+    const int x_lane = x_row < a.m ? (int)((int64_t)x_row * a.ldx * 2) + 16 * x_chunk : 0;
+    const int x_dead = x_row < a.m ? 0 : kOut;
+    // fragment f of lane (col, q) is chunk 4q + f of row col, k = 32q + 8f
+    // (rows 4..15 of the MFMA are never stored; they repeat rows 0..3)
+    const int x_src = ((col & 3) * 16 + 4 * q) * 4;
 
     uint32_t rc[D][W];
     uint32_t rm[D][MW];
-    u32x4_dev_t ra[D][4];
-    auto load = [&](int i, uint32_t (&c)[W], uint32_t (&mm)[MW], u32x4_dev_t (&av)[4]) {
+    u32x4_dev_t ra[D];
+    auto load = [&](int i, uint32_t (&c)[W], uint32_t (&mm)[MW], u32x4_dev_t& av) {
         const int kb = kb_begin + i;
-        const bool live = i < nkb;
-        const int co = live ? (kb * kWave + lane) * W * 4 : kOut;
+        // Offsets are computed unconditionally and pushed past the buffer by
+        // OR-ing kOut, with no select: a uniform condition around a load
+        // becomes a branch, and the wait-count pass drains every load in
+        // flight where the branches join.
+        const int dead = (int)((uint32_t)(nkb - 1 - i) >> 31) * kOut;  // kOut when i >= nkb
+        const int co = ((kb * kWave + lane) * W * 4) | dead;
         if constexpr (W == 4) {
             const u32x4_dev_t v = __builtin_amdgcn_raw_buffer_load_b128(codes, co, 0, 2);  // nt
             c[0] = v.x; c[1] = v.y; c[2] = v.z; c[3] = v.w;
@@ -679,7 +694,7 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
         } else {
             c[0] = __builtin_amdgcn_raw_buffer_load_b32(codes, co, 0, 2);
         }
-        const int mo = live ? ((kb / gpk) * 16 + col) * MW * 4 : kOut;
+        const int mo = (((kb / gpk) * 16 + col) * MW * 4) | dead;
         if constexpr (MW == 4) {
             const u32x4_dev_t v = __builtin_amdgcn_raw_buffer_load_b128(meta, mo, 0, 0);
             mm[0] = v.x; mm[1] = v.y; mm[2] = v.z; mm[3] = v.w;
@@ -687,12 +702,17 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b64(meta, mo, 0, 0);
             mm[0] = v[0]; mm[1] = v[1];
         }
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const int k0 = kb * kKBlock + 32 * q + 8 * f;
-            const int xo = live && k0 < a.k ? x_lane + (kb * kKBlock + 8 * f) * 2 : kOut;
-            av[f] = __builtin_bit_cast(u32x4_dev_t, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
-        }
+        const int k0 = kb * kKBlock + 8 * x_chunk;
+        const int past_k = (int)((uint32_t)(a.k - 1 - k0) >> 31) * kOut;  // kOut when k0 >= K
+        const int xo = (x_lane + kb * kKBlock * 2) | dead | past_k | x_dead;
+        av = __builtin_bit_cast(u32x4_dev_t, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0));
+    };
+    auto afrag = [&](const u32x4_dev_t& av, int f) {
+        const int src = x_src + 4 * f;
+        return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)av.x),
+                          (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)av.y),
+                          (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)av.z),
+                          (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)av.w));
     };
     floatx4_t acc = floatx4_t{0.f, 0.f, 0.f, 0.f};
     // Chunks of D k-blocks: every load of a chunk is issued before its first
@@ -712,7 +732,7 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
                 const uint4 bw = decode_fragment<BITS>(rc[st], f, tab);
-                acc = mfma16<F16>(__builtin_bit_cast(uint4, ra[st][f]), bw, acc);
+                acc = mfma16<F16>(afrag(ra[st], f), bw, acc);
             }
         }
     }
