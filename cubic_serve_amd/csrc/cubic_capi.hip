@@ -61,9 +61,15 @@ struct GemmPlan {
 };
 
 // Small-row regime (the reference's small_rows path, M <= 4): one tile per
-// workgroup, K split over the workgroup's waves; a function of k alone.
-bool small_rows(int64_t m, int bits, int group_in) {
-    return m >= 1 && m <= 4 && bits <= 4 && group_in > 0 && group_in % kKBlock == 0;
+// workgroup, K split over the workgroup's waves; a function of (k, bits) alone.
+// Above 4 bits a weight is evaluated from the curve (no prepared table), and
+// the small-row kernel only pays off while each wave's K range is short: at
+// most 64 k-blocks (Llama-3-70B qkv / o / gate-up at 6 and 8 bits 7-20 %
+// faster than the MFMA-tile kernel; the 28672-deep down projection 3-16 %
+// slower, so it stays on the MFMA-tile kernel).
+bool small_rows(int64_t m, int bits, int group_in, int64_t k) {
+    if (m < 1 || m > 4 || bits > 8 || group_in <= 0 || group_in % kKBlock != 0) return false;
+    return bits <= 4 || ceil_div(k, kKBlock) <= 64;
 }
 
 // K partition of one member: split in powers of two (at most 8) until a
@@ -90,7 +96,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
     p.rows_waves = 0;
-    if (small_rows(m, bits, group_in)) {
+    if (small_rows(m, bits, group_in, k)) {
         p.rows_waves = p.k_blocks > 32 ? 8 : 4;
         p.blocks_per_split = (int)ceil_div(p.k_blocks, p.rows_waves);
         p.split = 1;

@@ -639,6 +639,13 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
     constexpr int MW = meta_words<BITS>();
     constexpr int kOut = 0x7FFFFFF0;  // buffer offset past every range: the load returns 0, no fetch
     __shared__ float red[G][16][4];
+    // bits >= 5: the curve abscissae t_i = i / (2^(BITS-1) - 1), as the MFMA kernel builds them
+    __shared__ float t_lds[BITS >= 5 ? (1 << (BITS - 1)) : 1];
+    if constexpr (BITS >= 5) {
+        for (int i = threadIdx.x; i < (1 << (BITS - 1)); i += 64 * G)
+            t_lds[i] = (float)((double)i / (double)((1 << (BITS - 1)) - 1));
+        __syncthreads();
+    }
     // wave index as a scalar: the per-wave K range and loop bounds stay uniform
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -691,8 +698,24 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
         } else if constexpr (W == 3) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b96(codes, co, 0, 2);
             c[0] = v[0]; c[1] = v[1]; c[2] = v[2];
-        } else {
+        } else if constexpr (W == 1) {
             c[0] = __builtin_amdgcn_raw_buffer_load_b32(codes, co, 0, 2);
+        } else {  // 5..8 words: 16 bytes, then the rest (dword-aligned buffer loads)
+            const u32x4_dev_t v = __builtin_amdgcn_raw_buffer_load_b128(codes, co, 0, 2);
+            c[0] = v.x; c[1] = v.y; c[2] = v.z; c[3] = v.w;
+            const int co4 = co + 16;  // still past the buffer when dead
+            if constexpr (W == 5) {
+                c[4] = __builtin_amdgcn_raw_buffer_load_b32(codes, co4, 0, 2);
+            } else if constexpr (W == 6) {
+                const auto u = __builtin_amdgcn_raw_buffer_load_b64(codes, co4, 0, 2);
+                c[4] = u[0]; c[5] = u[1];
+            } else if constexpr (W == 7) {
+                const auto u = __builtin_amdgcn_raw_buffer_load_b96(codes, co4, 0, 2);
+                c[4] = u[0]; c[5] = u[1]; c[6] = u[2];
+            } else {
+                const u32x4_dev_t u = __builtin_amdgcn_raw_buffer_load_b128(codes, co4, 0, 2);
+                c[4] = u.x; c[5] = u.y; c[6] = u.z; c[7] = u.w;
+            }
         }
         const int mo = (((kb / gpk) * 16 + col) * MW * 4) | dead;
         if constexpr (MW == 4) {
@@ -725,13 +748,22 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
 #pragma unroll
         for (int st = 0; st < D; ++st) {
             LevelTable tab;
-            tab.lo_lo = rm[st][0];
-            tab.hi_lo = rm[st][1];
-            tab.lo_hi = MW == 4 ? rm[st][MW == 4 ? 2 : 0] : 0u;
-            tab.hi_hi = MW == 4 ? rm[st][MW == 4 ? 3 : 1] : 0u;
+            float ms = 0.0f, ma = 0.0f, mb = 0.0f;
+            if constexpr (BITS <= 4) {
+                tab.lo_lo = rm[st][0];
+                tab.hi_lo = rm[st][1];
+                tab.lo_hi = MW == 4 ? rm[st][MW == 4 ? 2 : 0] : 0u;
+                tab.hi_hi = MW == 4 ? rm[st][MW == 4 ? 3 : 1] : 0u;
+            } else {
+                ms = __uint_as_float(rm[st][0]);
+                ma = half_bits_to_float(rm[st][1] & 0xFFFFu);
+                mb = half_bits_to_float(rm[st][1] >> 16);
+            }
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
-                const uint4 bw = decode_fragment<BITS>(rc[st], f, tab);
+                uint4 bw;
+                if constexpr (BITS <= 4) bw = decode_fragment<BITS>(rc[st], f, tab);
+                else bw = direct_fragment<BITS, F16>(rc[st], f, ms, ma, mb, t_lds);
                 acc = mfma16<F16>(afrag(ra[st], f), bw, acc);
             }
         }
@@ -993,6 +1025,10 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
             case 2: return launch_rows_bits<2>(a, a.rows_waves, s);
             case 3: return launch_rows_bits<3>(a, a.rows_waves, s);
             case 4: return launch_rows_bits<4>(a, a.rows_waves, s);
+            case 5: return launch_rows_bits<5>(a, a.rows_waves, s);
+            case 6: return launch_rows_bits<6>(a, a.rows_waves, s);
+            case 7: return launch_rows_bits<7>(a, a.rows_waves, s);
+            case 8: return launch_rows_bits<8>(a, a.rows_waves, s);
             default: return hipErrorInvalidValue;
         }
     }

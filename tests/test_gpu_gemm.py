@@ -101,6 +101,24 @@ def test_identity_level_table_bits_exact(oracle, bits, gi, fmt):
     assert np.array_equal(canon_zero(got), canon_zero(oracle_decode_bits(oracle, m)))
 
 
+@pytest.mark.parametrize("bits", [5, 6, 7, 8])
+@pytest.mark.parametrize("gi,fmt", [(128, qz.FMT_F32), (256, FMTS[1]), (128, FMTS[2])])
+def test_identity_small_rows_curve_bits_exact(oracle, bits, gi, fmt):
+    """Above 4 bits the small-row kernel (M <= 4, K <= 64 k-blocks) evaluates
+    every weight from the curve: [4, k] slices of the identity give
+    bf16(decode_cubic) for every code, a group spanning two k-blocks and a K
+    tail included."""
+    n, k = 40, 600
+    print(f"small-row identity bits={bits} gi={gi} fmt={fmt}", flush=True)
+    m = random_matrix(n, k, bits, gi, fmt, seed=bits * 7 + gi + FMTS.index(fmt), partitions=(24, 16))
+    md = m.to(DEV)
+    ops = linear.PackedLinearOperators()
+    eye = torch.eye(k, dtype=torch.bfloat16, device=DEV)
+    y = torch.cat([ops.linear(eye[r:r + 4].contiguous(), md) for r in range(0, k, 4)])
+    got = to_bits(y.T.contiguous())
+    assert np.array_equal(canon_zero(got), canon_zero(oracle_decode_bits(oracle, m)))
+
+
 @pytest.mark.parametrize("k,gi", [(200, 32), (384, 256), (136, 128)])
 def test_identity_partial_groups_and_k_tails(oracle, k, gi):
     m = random_matrix(33, k, 4, gi, qz.FMT_F32, seed=k)

@@ -35,8 +35,9 @@ def decode_f16_bits(oracle, m: qz.QuantizedMatrix) -> np.ndarray:
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("rows", [4, 64])
 def test_identity_contraction_is_exact_f16_decode(oracle, bits, fmt, rows):
-    """rows = 4 runs the small-row kernel (bits <= 4) on [4, k] slices of the
-    identity; rows = 64 the MFMA tile path."""
+    """rows = 4 runs the small-row kernel on [4, k] slices of the identity
+    (groups of 128: bits 1, 3, 5, 7; groups of 64 stay on the MFMA tile
+    path); rows = 64 the MFMA tile path."""
     n, k, gi = 72, 256, 128 if bits % 2 else 64
     print(f"f16 identity bits={bits} fmt={fmt} rows={rows}", flush=True)
     m = random_matrix(n, k, bits, gi, fmt, seed=bits * 10 + FMTS.index(fmt), partitions=(40, 32))

@@ -83,12 +83,13 @@ def test_row_invariant_across_m_past_one_chunk(n, k):
         assert torch.equal(_bits16(y[m - 1:m]), _bits16(last)), m
 
 
+@pytest.mark.parametrize("bits", [4, 6, 8])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (32768, 2048), (48, 4352), (256, 2176)])
-def test_small_rows_regime_invariant_and_enclosed(oracle, n, k):
+def test_small_rows_regime_invariant_and_enclosed(oracle, n, k, bits):
     """Small-row kernel (M <= 4): every row equal across M = 1..4 and to a
     permuted launch, outputs inside the FP64 enclosure (K tails included)."""
-    print(f"small rows n={n} k={k}", flush=True)
-    w = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(n * 3 + k)) * 0.02, 4)
+    print(f"small rows n={n} k={k} bits={bits}", flush=True)
+    w = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(n * 3 + k)) * 0.02, bits)
     wd = w.to(DEV)
     ops = linear.PackedLinearOperators()
     x = torch.randn((4, k), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV)
