@@ -90,8 +90,12 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  * K plan: the K partition of every output column is a function of its
  * member's (n, k) only -- never of m, nor of how many members share a launch
  * (quantization/extensions/cubic/marlin.py:347-360, common/marlin/cost.py:
- * 59-79) -- so a row's result is bitwise the same for every m and grouped
- * members equal separate launches bit for bit.
+ * 59-79) -- so a row's result is bitwise the same for every m of one
+ * arithmetic regime and grouped members equal separate launches bit for bit.
+ * The regimes, as the reference's: m <= 4 with groups of whole 128-wide
+ * k-blocks runs the small-row kernel (bits <= 4 at any k; 5..8 bits while k
+ * is at most 64 k-blocks), one partition per wave, a function of k alone;
+ * every other m runs the MFMA-tile kernel with the K plan above.
  *
  * cubic_gemm_workspace_bytes: workspace for (m, n, k); 0 when no K split.
  *   The workspace must be zero-filled before its first use; every completed
