@@ -62,14 +62,16 @@ struct GemmPlan {
 
 // Small-row regime (the reference's small_rows path, M <= 4): one tile per
 // workgroup, K split over the workgroup's waves; a function of (k, bits) alone.
-// Above 4 bits a weight is evaluated from the curve (no prepared table), and
-// the small-row kernel only pays off while each wave's K range is short: at
-// most 64 k-blocks (Llama-3-70B qkv / o / gate-up at 6 and 8 bits 7-20 %
-// faster than the MFMA-tile kernel; the 28672-deep down projection 3-16 %
-// slower, so it stays on the MFMA-tile kernel).
+// Above 4 bits there is no prepared table: 5-6 bits build each k-block's
+// levels in LDS, 7-8 bits evaluate every weight from the curve.  Measured
+// against the MFMA-tile kernel at M = 1 (Llama-3-70B linears, Qwen3 lm_head):
+// 7-8 bits win at every K (down 28672-deep: 95 -> 81 us at 7 bits); 5-6 bits
+// win up to 64 k-blocks (gate/up 145 -> 121 us at 5 bits) and lose a few
+// percent on the 224-k-block down projection, which stays on the MFMA-tile
+// kernel.
 bool small_rows(int64_t m, int bits, int group_in, int64_t k) {
     if (m < 1 || m > 4 || bits > 8 || group_in <= 0 || group_in % kKBlock != 0) return false;
-    return bits <= 4 || ceil_div(k, kKBlock) <= 64;
+    return bits <= 4 || bits >= 7 || ceil_div(k, kKBlock) <= 64;
 }
 
 // K partition of one member: split in powers of two (at most 8) until a

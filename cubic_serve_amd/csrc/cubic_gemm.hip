@@ -641,6 +641,14 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
     __shared__ float red[G][16][4];
     // bits >= 5: the curve abscissae t_i = i / (2^(BITS-1) - 1), as the MFMA kernel builds them
     __shared__ float t_lds[BITS >= 5 ? (1 << (BITS - 1)) : 1];
+    // bits 5..6: per wave, the current k-block's group levels of the tile's
+    // 16 columns (wave-private, rebuilt every k-block; rows padded as in the
+    // MFMA kernel).  At 7 and 8 bits a column has 64-128 levels, as many as
+    // the lane has weights per k-block, and direct evaluation measured faster.
+    constexpr bool LT = BITS >= 5 && BITS <= 6;
+    constexpr int NM = 1 << (BITS - 1);
+    constexpr int NMP = NM + 4;
+    __shared__ __attribute__((aligned(16))) uint16_t lv_lds[LT ? G * 16 * NMP : 1];
     if constexpr (BITS >= 5) {
         for (int i = threadIdx.x; i < (1 << (BITS - 1)); i += 64 * G)
             t_lds[i] = (float)((double)i / (double)((1 << (BITS - 1)) - 1));
@@ -759,10 +767,35 @@ __global__ __launch_bounds__(64 * G) void rows_kernel(GemmArgs a) {
                 ma = half_bits_to_float(rm[st][1] & 0xFFFFu);
                 mb = half_bits_to_float(rm[st][1] >> 16);
             }
+            uint16_t* lv = &lv_lds[(wave * 16 + col) * NMP];
+            if constexpr (LT) {
+                // the four lanes of a column evaluate a quarter of its levels
+                // each, rounded as direct_fragment rounds them; the previous
+                // k-block's lookups are complete before the table is rewritten
+                constexpr int kPer = NM / 4;
+                uint32_t pairs[kPer / 2];
+#pragma unroll
+                for (int p = 0; p < kPer / 2; ++p) {
+                    const int m = q * kPer + 2 * p;
+                    pairs[p] = pack_level2<F16>(curve_level(t_lds[m], ms, ma, mb),
+                                                curve_level(t_lds[m + 1], ms, ma, mb));
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                uint32_t* dst = reinterpret_cast<uint32_t*>(lv + q * kPer);
+#pragma unroll
+                for (int p = 0; p < kPer / 2; p += 2)
+                    *reinterpret_cast<uint2*>(dst + p) = make_uint2(pairs[p], pairs[p + 1]);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
                 uint4 bw;
                 if constexpr (BITS <= 4) bw = decode_fragment<BITS>(rc[st], f, tab);
+                else if constexpr (LT) bw = table_fragment<BITS>(rc[st], f, lv);
                 else bw = direct_fragment<BITS, F16>(rc[st], f, ms, ma, mb, t_lds);
                 acc = mfma16<F16>(afrag(ra[st], f), bw, acc);
             }

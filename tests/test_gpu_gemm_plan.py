@@ -84,10 +84,12 @@ def test_row_invariant_across_m_past_one_chunk(n, k):
 
 
 @pytest.mark.parametrize("bits", [4, 6, 8])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (32768, 2048), (48, 4352), (256, 2176)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (32768, 2048), (48, 4352), (256, 2176), (144, 8320)])
 def test_small_rows_regime_invariant_and_enclosed(oracle, n, k, bits):
-    """Small-row kernel (M <= 4): every row equal across M = 1..4 and to a
-    permuted launch, outputs inside the FP64 enclosure (K tails included)."""
+    """Small-row regime (M <= 4): every row equal across M = 1..4 and to a
+    permuted launch, outputs inside the FP64 enclosure (K tails included).
+    k = 8320 is 65 k-blocks: 6 bits run the MFMA-tile kernel there, 4 and 8
+    bits the small-row kernel."""
     print(f"small rows n={n} k={k} bits={bits}", flush=True)
     w = qz.quantize_cubic(torch.randn((n, k), generator=torch.Generator().manual_seed(n * 3 + k)) * 0.02, bits)
     wd = w.to(DEV)
