@@ -574,6 +574,12 @@ void gemm_kernel(GemmArgs a) {
             };
             // A fragments are double-buffered: the LDS reads of fragment f + 1
             // are in flight while fragment f is decoded and multiplied.
+            // Raised wave priority over the fragment reads, decode and MFMA:
+            // the arbiter then favours a wave that is in its math phase over
+            // one issuing loads or staging activations, which keeps the MFMA
+            // pipe fed while other waves wait on memory (cfg2 gate/up 30.1 ->
+            // 29.2 us, qkv 14.8 -> 14.5 us, same box).
+            __builtin_amdgcn_s_setprio(1);
             bf16x8_t afrag_buf[2][MT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) afrag_buf[0][mt] = afrag_at(mt, 0);
@@ -598,6 +604,7 @@ void gemm_kernel(GemmArgs a) {
                         acc[mt][j] = mfma16<F16>(__builtin_bit_cast(uint4, afrag_buf[fb][mt]), bw, acc[mt][j]);
                 }
             }
+            __builtin_amdgcn_s_setprio(0);
             // Refill this ring slot only now that its codes are consumed: a load
             // issued while the old value is live would land in other registers
             // and be copied back (a wait on the load) at the loop edge.
