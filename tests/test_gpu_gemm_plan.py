@@ -106,7 +106,7 @@ def test_small_rows_regime_invariant_and_enclosed(oracle, n, k, bits):
         _check_linear(oracle, part, x, y4[:, start:start + cols].contiguous())
 
 
-@pytest.mark.parametrize("m", [1, 64, 130])
+@pytest.mark.parametrize("m", [1, 8, 64, 130])
 def test_grouped_equals_separate_llama70b_gate_up(m):
     """cfg5 gate/up: two 28672 x 8192 members in one launch equal separate launches."""
     print(f"cfg5 gate/up grouped == separate m={m}", flush=True)
@@ -163,3 +163,30 @@ def test_cfg3_w3_lm_head_m256_sampled_enclosure(oracle):
         for rows in (slice(0, 64), slice(192, 256)):
             print(f"cfg3 lm_head cols {start} rows {rows}", flush=True)
             _check_linear(oracle, part, x[rows].contiguous(), y[rows, start:start + 64].contiguous())
+
+
+@pytest.mark.parametrize("n,k,gi,bits", [
+    (4096, 4096, 128, 4),    # split 4, even partitions
+    (48, 4352, 128, 4),      # split 8, odd partitions (a pad block each)
+    (6144, 4096, 64, 3),     # per-quarter groups
+    (256, 2176, 32, 2),      # K tail, groups of 32
+    (24576, 1024, 128, 1),   # split 1
+])
+@pytest.mark.parametrize("f16", [False, True])
+def test_sixteen_rows_equal_mfma_tile_rows(n, k, gi, bits, f16):
+    """One m-tile (5..16 rows) and two (17 rows) of the MFMA-tile kernel:
+    the first 16 rows of an M = 17 launch equal an M = 16 launch and every
+    shorter prefix bit for bit, at even and odd K partitions (pad blocks),
+    per-quarter groups, K tails, split 1 and fp16."""
+    print(f"16 vs 17 rows n={n} k={k} gi={gi} bits={bits} f16={f16}", flush=True)
+    dt = torch.float16 if f16 else torch.bfloat16
+    w = random_matrix(n, k, bits, gi, qz.FMT_F32, seed=n + k + bits, partitions=(n // 2, n - n // 2))
+    prepared = linear.prepare_matrix(w.to(DEV), DEV, dt)
+    x = torch.randn((17, k), generator=torch.Generator().manual_seed(k)).to(dt).to(DEV)
+    def run(rows):
+        y = torch.empty((rows, n), dtype=dt, device=DEV)
+        linear.bind_prepared(x[:rows].contiguous(), prepared, (y,)).launch()
+        return y
+    y17 = run(17)
+    for rows in (16, 11, 5):
+        assert torch.equal(_bits16(run(rows)), _bits16(y17[:rows])), rows
