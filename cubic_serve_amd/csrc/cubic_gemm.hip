@@ -625,10 +625,12 @@ void gemm_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Small-row GEMM (M <= 4; bits <= 4; groups of whole k-blocks)
+// Small-row GEMM (M <= 4; groups of whole k-blocks; bits <= 4 and 7..8 at any K,
+// 5..6 up to 64 k-blocks -- the host plan decides)
 //   grid.x: 16-column tiles; a workgroup of G waves owns one tile and all of K.
 //   Wave w streams the tile's k-blocks [w * kbw, (w + 1) * kbw) in chunks of
-//   D: codes, the group's level table and the k-block's 4 x 128 activations
+//   D: codes, the group's level table (bits <= 4) or curve parameters, and
+//   the k-block's 4 x 128 activations
 //   (one 16-byte load per lane; rows past M read zero), all loaded straight
 //   into registers -- no LDS staging and no barrier in the loop.  The MFMA
 //   A fragments are gathered across lanes with ds_bpermute: the loop is
@@ -1059,7 +1061,7 @@ hipError_t launch_bits(const GemmArgs& a, int mt, int j, dim3 grid, hipStream_t 
 // host plan: J from n, the K split from the number of output blocks (so a
 // row's result is the same for every m up to one 64-row chunk).
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-    if (a.rows_waves > 0) {  // small-row plan (host: M <= 4, bits <= 4, whole-k-block groups)
+    if (a.rows_waves > 0) {  // small-row plan (host: M <= 4, whole-k-block groups)
         switch (a.bits) {
             case 1: return launch_rows_bits<1>(a, a.rows_waves, s);
             case 2: return launch_rows_bits<2>(a, a.rows_waves, s);
