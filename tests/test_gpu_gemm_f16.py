@@ -50,6 +50,22 @@ def test_identity_contraction_is_exact_f16_decode(oracle, bits, fmt, rows):
     assert np.array_equal(canon_zero(got), canon_zero(decode_f16_bits(oracle, m)))
 
 
+@pytest.mark.parametrize("bits", [6, 8])
+def test_identity_small_rows_curve_bits_f16(oracle, bits):
+    """fp16 through the small-row kernel at 6 bits (level tables in LDS) and
+    8 bits (curve evaluated per weight): [4, k] identity slices give
+    fp16(decode) for every code."""
+    n, k, gi = 40, 600, 128
+    print(f"f16 small-row identity bits={bits}", flush=True)
+    m = random_matrix(n, k, bits, gi, qz.FMT_F32, seed=bits * 31, partitions=(24, 16))
+    md = m.to(DEV)
+    ops = linear.PackedLinearOperators()
+    eye = torch.eye(k, dtype=torch.float16, device=DEV)
+    y = torch.cat([ops.linear(eye[r:r + 4].contiguous(), md) for r in range(0, k, 4)])
+    got = to_bits(y.T.contiguous())
+    assert np.array_equal(canon_zero(got), canon_zero(decode_f16_bits(oracle, m)))
+
+
 @pytest.mark.parametrize("bits,gi", [(5, 128), (6, 256), (7, 128)])
 def test_identity_level_tables_f16(oracle, bits, gi):
     n, k = 40, 600
