@@ -18,7 +18,7 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 LIB_DIR = PACKAGE / "_lib"
 LIB = LIB_DIR / "libcubic_mi355x.so"
-SOURCES = ("cubic_capi.hip", "cubic_gemm.hip", "cubic_accept.hip", "cubic_embed.hip", "cubic_moe.hip",
+SOURCES = ("cubic_capi.hip", "cubic_gemm.hip", "cubic_panel.hip", "cubic_accept.hip", "cubic_embed.hip", "cubic_moe.hip",
            "cubic_greedy.hip")
 ARCH = "gfx950"
 # Per-source flags.  The acceptance kernel sizes its LDS for three workgroups

@@ -58,7 +58,18 @@ struct GemmPlan {
     int n_tiles, k_blocks, tiles_per_wave, col_blocks, split, blocks_per_split;
     int chunk_rows;  // rows per grid-z chunk (64; 32 when M is split across workgroups; 128 past 64 rows)
     int rows_waves;  // > 0: small-row kernel, this many waves per tile, blocks_per_split per wave
+    int panel;       // > 0: column-panel kernel (2: level tables staged in LDS)
+    int panel_stages;  // column-panel ring depth
+    int panel_waves;   // column-panel waves per workgroup
 };
+
+#ifdef CUBIC_EXPERIMENTS
+// experiment builds only: force the panel plan (J, split, tables in LDS)
+static int g_exp_j = 0, g_exp_split = 0, g_exp_tl = -1, g_exp_panel = -1, g_exp_stages = 0, g_exp_waves = 0;
+extern "C" __attribute__((visibility("default"))) void cubic_exp_plan(int j, int split, int tl, int panel, int stages, int waves) {
+    g_exp_j = j; g_exp_split = split; g_exp_tl = tl; g_exp_panel = panel; g_exp_stages = stages; g_exp_waves = waves;
+}
+#endif
 
 // Small-row regime (the reference's small_rows path, M <= 4): one tile per
 // workgroup, K split over the workgroup's waves; a function of (k, bits) alone.
@@ -93,7 +104,7 @@ void plan_k(int64_t n_member, int64_t k, int* split_out, int* bps_out) {
 }
 
 GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits, int group_in) {
-    GemmPlan p;
+    GemmPlan p = {};
     const int64_t n = n_member * members;
     p.n_tiles = (int)ceil_div(n, 16);
     p.k_blocks = (int)ceil_div(k, kKBlock);
@@ -107,7 +118,45 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
         p.chunk_rows = 4;
         return p;
     }
+    p.panel = 0;
+    p.panel_stages = 2;
+    p.panel_waves = cubic::kGemmWaves;
     plan_k(n_member, k, &p.split, &p.blocks_per_split);
+#ifdef CUBIC_EXPERIMENTS
+    if (g_exp_split > 0) {
+        p.split = g_exp_split;
+        p.blocks_per_split = (int)ceil_div(p.k_blocks, p.split);
+        p.split = (int)ceil_div(p.k_blocks, p.blocks_per_split);
+    }
+#endif
+    // Column panels (M <= 64, bits <= 4, whole-k-block groups): the tiles of
+    // a wave share each staged activation block and A fragment.  The
+    // kernel addresses activations and metadata with 32-bit buffer offsets.
+    const int64_t meta_bytes = (int64_t)p.n_tiles * ceil_div(k, group_in) * 16 * (bits == 4 ? 16 : 8);
+    if (m <= 64 && bits <= 4 && group_in % kKBlock == 0 && meta_bytes < (int64_t(1) << 31)) {
+        p.panel = bits == 4 ? 2 : 1;
+        // Two tiles per wave (each staged activation block feeds twice the
+        // MFMAs) while the grid keeps >= 384 workgroups, with a 2-deep ring;
+        // one tile per wave otherwise, with a 4-deep ring.  Measured at
+        // M = 64, 4 bits, Llama-3-8B shapes: gate/up 26.7 us (one tile per
+        // wave in gemm_kernel: 29.9), lm_head 110 (116), down 18.2 (19.2),
+        // qkv and o equal; two tiles with a 4-deep ring: lm_head 143.
+        int j = ceil_div(p.n_tiles, cubic::kGemmWaves * 2) * p.split >= 384 ? 2 : 1;
+        p.panel_stages = j == 2 ? 2 : 4;
+#ifdef CUBIC_EXPERIMENTS
+        if (g_exp_j > 0) j = g_exp_j;
+        if (g_exp_tl >= 0) p.panel = g_exp_tl ? 2 : 1;
+        if (g_exp_panel == 0) p.panel = 0;
+        if (g_exp_stages > 0) p.panel_stages = g_exp_stages;
+        if (g_exp_waves > 0) p.panel_waves = g_exp_waves;
+#endif
+        if (p.panel) {
+            p.tiles_per_wave = j;
+            p.col_blocks = (int)ceil_div(p.n_tiles, p.panel_waves * j);
+            p.chunk_rows = 64;
+            return p;
+        }
+    }
     // Past 64 rows (whole-k-block groups) a workgroup takes 128 rows: each
     // decoded weight fragment feeds eight m-tiles of MFMA instead of four.
     const bool wide = m > 64 && group_in % kKBlock == 0;
@@ -132,14 +181,15 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
 }
 
 // Split-K workspace: arrival counters per output block, then FP32 partials
-// per K partition and output block (64-row chunk x column block): kGemmWaves
-// waves x J tiles x MT m-tiles x 64 lanes float4 units.
+// per K partition and output block (64-row chunk x column block): waves x J
+// tiles x MT m-tiles x 64 lanes float4 units.
 int64_t gemm_workspace(int64_t m, int64_t n_member, int members, int64_t k, int bits, int group_in) {
     const GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
     if (p.split == 1) return 0;
     const int64_t blocks = (int64_t)p.col_blocks * ceil_div(m, p.chunk_rows);
     const int64_t mt = p.chunk_rows == 128 ? 8 : p.chunk_rows == 32 ? 2 : (ceil_div(m, 64) > 1 ? 4 : (m >= 33 ? 4 : (m >= 17 ? 2 : 1)));
-    const int64_t units = cubic::kGemmWaves * p.tiles_per_wave * mt * 64;
+    const int64_t units = (p.panel ? p.panel_waves : cubic::kGemmWaves) *
+                          p.tiles_per_wave * mt * 64;
     return align256(blocks * 4) + align256((int64_t)p.split * blocks * units * 16);
 }
 
@@ -172,9 +222,22 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
         return fail(CUBIC_ENOTSUP, "activations need k %% 8 == 0, ldx %% 8 == 0 and 16-byte alignment");
     for (int i = 0; i < members; ++i)
         if (ldys[i] < n_member) return fail(CUBIC_EINVAL, "output leading dimension too small");
-    const GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
+    GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
     const int64_t need = gemm_workspace(m, n_member, members, k, bits, group_in);
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
+    if (p.panel && m * ldx * 2 >= (int64_t(1) << 31)) {
+        // the column-panel kernel reaches activations through 32-bit buffer
+        // offsets: a row stride this large takes the MFMA-tile kernel (same
+        // K plan, same arithmetic), whose split-K buffer is no larger
+        p.panel = 0;
+        p.tiles_per_wave = 1;
+        p.col_blocks = (int)ceil_div(p.n_tiles, cubic::kGemmWaves);
+        p.chunk_rows = 64;
+        const int64_t alt = p.split == 1 ? 0
+                          : align256((int64_t)p.col_blocks * 4) +
+                                align256((int64_t)p.split * p.col_blocks * cubic::kGemmWaves * 4 * 64 * 16);
+        if (workspace_bytes < alt) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)alt);
+    }
     if (need && !workspace) return fail(CUBIC_EINVAL, "null workspace");
     cubic::GemmArgs a = {};
     a.x = (const uint16_t*)x;
@@ -199,6 +262,9 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
     a.tiles_per_wave = p.tiles_per_wave;
     a.chunk_rows = p.chunk_rows;
     a.rows_waves = p.rows_waves;
+    a.panel = p.panel;
+    a.panel_stages = p.panel_stages;
+    a.panel_waves = p.panel_waves;
     a.f16 = dtype == CUBIC_DTYPE_F16;
     if (p.split > 1) {
         const int64_t counters = align256((int64_t)p.col_blocks * ceil_div(m, p.chunk_rows) * 4);  // one per output block

@@ -136,6 +136,9 @@ struct GemmArgs {
     int rows_waves;               // > 0: small-row kernel with this many waves per tile
                                   // (blocks_per_split = k-blocks per wave)
     int f16;                      // activations, prepared levels and outputs are fp16 (else bf16)
+    int panel;                    // > 0: column-panel kernel (2: level tables staged in LDS)
+    int panel_stages;             // column-panel ring depth S (2 or 4; divides the partition's k-block pairs)
+    int panel_waves;              // column-panel waves per workgroup (the kernels take 4)
     // routed experts (MoE, routed != 0): workgroup chunk z covers the
     // 16 * MT padded route slots [z * 16 * MT, ...) of one expert
     // (block_expert[z]); a slot holds a route ordinal, or `routes` for
@@ -233,6 +236,8 @@ hipError_t launch_prepare(const void* packed, const float* scale, const uint16_t
                           const uint16_t* b, int64_t n, int64_t k, int bits, int group_in, int f16,
                           uint32_t* codes, uint32_t* meta, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Column-panel kernel (cubic_panel.hip), chosen by the host plan (a.panel > 0).
+hipError_t launch_panel_gemm(const GemmArgs& a, hipStream_t s);
 // Routed-block table from compact routes (quantization/common/marlin/repack.py:253-277)
 hipError_t launch_pad_routes(const int32_t* counts, const int32_t* starts, const int32_t* block_starts,
                              const int32_t* total_blocks, const int32_t* row_map, int experts,
