@@ -82,6 +82,10 @@ extern "C" __attribute__((visibility("default"))) void cubic_exp_plan(int j, int
 // kernel.
 bool small_rows(int64_t m, int bits, int group_in, int64_t k) {
     if (m < 1 || m > 4 || bits > 8 || group_in <= 0 || group_in % kKBlock != 0) return false;
+    // the small-row kernel sizes a tile's code and metadata buffers in 32 bits
+    const int64_t k_blocks = ceil_div(k, kKBlock);
+    if (k_blocks * 64 * bits * 4 >= (int64_t(1) << 31) || ceil_div(k, group_in) * 16 * 16 >= (int64_t(1) << 31))
+        return false;
     return bits <= 4 || bits >= 7 || ceil_div(k, kKBlock) <= 64;
 }
 
@@ -225,6 +229,9 @@ int gemm_common(const void* x, int64_t ldx, const uint32_t* codes, const uint32_
     GemmPlan p = plan_gemm(m, n_member, members, k, bits, group_in);
     const int64_t need = gemm_workspace(m, n_member, members, k, bits, group_in);
     if (workspace_bytes < need) return fail(CUBIC_EWORKSPACE, "gemm workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
+    if (p.rows_waves && m * ldx * 2 >= (int64_t(1) << 31))
+        return fail(CUBIC_ENOTSUP, "small-row GEMM: activation row stride too large (m * ldx * 2 = %lld >= 2^31 bytes)",
+                    (long long)(m * ldx * 2));
     if (p.panel && m * ldx * 2 >= (int64_t(1) << 31)) {
         // the column-panel kernel reaches activations through 32-bit buffer
         // offsets: a row stride this large takes the MFMA-tile kernel (same
@@ -335,25 +342,21 @@ int next_pow2(int v) {
 // survivor keys and flags, in device memory that the library owns for the life
 // of the process (one copy per device).  The name below is a host-side handle;
 // device code only ever sees the address hipGetSymbolAddress returns for the
-// current device.  Launches leave the counters zero, as cubic_accept does; the
-// array starts zero (zero-initialised device global) and set-up clears it once
-// per device with a fill kernel.
+// current device.  The array starts zero (a zero-initialised device global)
+// and every launch leaves its counters zero again, as cubic_accept does with
+// its workspace, so set-up only resolves the address: it enqueues nothing, and
+// a first call made under HIP graph capture records only the acceptance
+// launches themselves.
 // ---------------------------------------------------------------------------
 constexpr int64_t kAcceptScratchBytes = int64_t(4) << 20;
 __device__ __align__(256) uint32_t scratch[kAcceptScratchBytes / 4];
-
-__global__ void clear_words_kernel(uint32_t* p, int64_t words) {
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words;
-         i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
-}
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices];
 
-// Address of the current device's scratch; set up on the first call per device.
-int accept_scratch(hipStream_t stream, void** out) {
+// Address of the current device's scratch, resolved on the first call per device.
+int accept_scratch(void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
@@ -363,9 +366,6 @@ int accept_scratch(hipStream_t stream, void** out) {
         void* ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
-        clear_words_kernel<<<256, 256, 0, stream>>>((uint32_t*)ptr, kAcceptScratchBytes / 4);
-        e = hipGetLastError();
-        if (e != hipSuccess) return hip_status(e, "scratch clear launch");
         g_scratch_ptr[dev] = ptr;
     }
     *out = g_scratch_ptr[dev];
@@ -1011,7 +1011,7 @@ int cubic_accept_noalloc(const void* logits, int64_t row_stride, int width, int 
                         (long long)need, (long long)kAcceptScratchBytes);
     }
     void* scratch_ptr = nullptr;
-    const int rc = accept_scratch((hipStream_t)stream, &scratch_ptr);
+    const int rc = accept_scratch(&scratch_ptr);
     if (rc != CUBIC_OK) return rc;
     return accept_common(logits, row_stride, width, c, depth, live_rows, live_count, row_temperatures, q_scores,
                          q_ids, capacity, draft_tokens, temperatures, top_ps, top_ks, seeds, ordinals,

@@ -406,8 +406,10 @@ CUBIC_API int cubic_accept(const void* logits, int64_t row_stride, int width, in
  * forbid hipMalloc).  Same operands, results and errors as cubic_accept.
  * Its scratch is a 4 MiB static device array per GPU, held until the process
  * ends; calls whose plan needs more (cubic_accept_workspace_bytes(c, depth,
- * width) > 4 MiB) fail with CUBIC_EWORKSPACE.  The first call on a device
- * resolves and clears that device's array.  Nothing here calls hipMalloc,
+ * width) > 4 MiB) fail with CUBIC_EWORKSPACE.  The array starts zero and
+ * every launch leaves its counters zero; the first call on a device only
+ * resolves the array's address and enqueues nothing besides the acceptance
+ * launches, so that call may itself be under capture.  Nothing here calls hipMalloc,
  * hipFree or an allocating library routine.  Every call on one GPU shares the
  * array and it keeps the last call's contents: calls that overlap on one GPU
  * (launches on concurrent streams) race and must be ordered by the caller.

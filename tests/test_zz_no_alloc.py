@@ -87,3 +87,63 @@ def test_noalloc_rejects_plans_beyond_the_static_scratch():
     rc = lib.cubic_accept_noalloc(*([0] * 2), width, c, depth, c, *([0] * 4), 20, *([0] * 13))
     assert rc == -4
     assert b"static scratch" in lib.cubic_last_error()
+
+
+def _capture_first_main():
+    """Run in a fresh process: the first cubic_accept_noalloc call on the device
+    is made under HIP graph capture; every replay must match cubic_accept."""
+    c, depth, width, k = 16, 3, 32768, 20
+    logits, q_scores, q_ids, params = _case(c, depth, width, k, 0.7, seed=21)
+    dev = {key: v.to(DEV) for key, v in params.items()}
+    plan = sampling.MTPVerifyPlan(logits=logits.to(DEV), q_scores=q_scores.to(DEV),
+                                  q_token_ids=q_ids.to(DEV), **dev)
+    plan.launch()
+    torch.cuda.synchronize()
+    want = [plan.candidate_scores.view(torch.int16).clone(), plan.candidate_ids.clone(),
+            plan.decisions.clone(), plan.merged.clone(), plan.emitted.clone()]
+    rows = c * (depth + 1)
+    out = [torch.empty((rows, k), dtype=torch.int16, device=DEV),
+           torch.empty((rows, k), dtype=torch.int64, device=DEV),
+           torch.empty((depth, c, 2), dtype=torch.int64, device=DEV),
+           torch.empty((c, 2), dtype=torch.int64, device=DEV),
+           torch.empty((c, depth + 1), dtype=torch.int64, device=DEV)]
+    for t in out:
+        t.fill_(-7)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _native.lib().cubic_accept_noalloc(
+            plan.logits.data_ptr(), plan.logits.stride(0), plan.width, c, depth, c, None,
+            plan.row_temperatures.data_ptr(), plan.q_scores.data_ptr(), plan.q_token_ids.data_ptr(), k,
+            dev["draft_tokens"].data_ptr(), dev["temperatures"].data_ptr(), dev["top_ps"].data_ptr(),
+            dev["top_ks"].data_ptr(), dev["seeds"].data_ptr(), dev["ordinals"].data_ptr(),
+            dev["uniforms"].data_ptr(), out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+            out[3].data_ptr(), out[4].data_ptr(), _native.stream_of(DEV))
+        assert rc == 0, _native.lib().cubic_last_error()
+    torch.cuda.synchronize()
+    # capture ran nothing
+    assert all(bool((t == -7).all()) for t in out)
+    for replay in range(3):
+        for t in out:
+            t.fill_(-7)
+        plan.launch()  # the workspace entry point, eagerly, between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for w, g in zip(want, out):
+            assert torch.equal(w.cpu(), g.cpu()), f"replay {replay}"
+    print("capture-first OK", flush=True)
+
+
+def test_noalloc_first_call_under_graph_capture():
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    print("noalloc: first call under capture, c=16 depth=3 V=32768, 3 replays (fresh process)", flush=True)
+    here = Path(__file__).resolve().parent
+    res = subprocess.run([sys.executable, "-c", "import test_zz_no_alloc as t; t._capture_first_main()"],
+                         cwd=here, env={**__import__("os").environ, "PYTHONPATH": str(here.parent)},
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=110)
+    out = res.stdout.decode(errors="replace")
+    assert res.returncode == 0 and "capture-first OK" in out, out[-3000:]
