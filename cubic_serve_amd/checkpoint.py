@@ -183,7 +183,8 @@ class QuantizationConfig:
     rules: tuple[EncodingRule, ...]
     ignored: tuple[str, ...]
     source_scope: str            # "root" or "text_config"
-    digest: str                  # identity of the declaration (sha256 of its canonical JSON)
+    digest: str                  # identity of the declaration: "b2s256:" + BLAKE2s-256 of its canonical JSON
+                                 # (models/quantization.py:117-119)
     table: RuleTable = field(repr=False, compare=False, default=None)
 
     @classmethod
@@ -209,7 +210,7 @@ class QuantizationConfig:
         rules, ignored = parse_config(declared)
         canonical = json.dumps(declared, sort_keys=True, separators=(",", ":"), allow_nan=False)
         return cls(method, rules, ignored, "root" if root is not None else "text_config",
-                   "sha256:" + hashlib.sha256(canonical.encode()).hexdigest(),
+                   "b2s256:" + hashlib.blake2s(canonical.encode()).hexdigest(),
                    RuleTable(rules, ignored))
 
     def resolve(self, module: str, *, aliases: tuple[str, ...] = (),
@@ -219,11 +220,12 @@ class QuantizationConfig:
         if operation not in CLASS_TARGETS:
             raise QuantizationError(f"unknown quantized consumer {operation!r}")
         names = [module, *aliases]
-        if self.source_scope == "text_config":
+        if self.source_scope == "text_config" and module.startswith("model.language_model."):
             # a text_config declaration names the language model's modules
-            # without the multimodal wrapper prefix
-            names = [n.replace("model.language_model.", "model.") if n.startswith("model.language_model.")
-                     else n for n in names]
+            # without the multimodal wrapper prefix: when the consumer itself
+            # sits under the wrapper, every name (aliases included) drops it;
+            # otherwise no name is rewritten (models/quantization.py:131-136)
+            names = [n.replace("model.language_model.", "model.") for n in names]
         if any(self.table.ignored(n) for n in names):
             return None
         best, chosen = None, set()

@@ -52,6 +52,13 @@ def test_invalid_arguments_fail_before_any_launch():
         _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 100, 0, 16, 4096, None, 0, None)
     with pytest.raises(ValueError, match="dtype"):
         _native.call("cubic_gemm", 16, 4096, 16, 16, 64, 4096, 4096, 4, 128, 2, 16, 4096, None, 0, None)
+    # the small-row kernel (M <= 4, no workspace) sizes a tile's codes in 32
+    # bits: at 2^31 bytes per tile (8 bits, K = 2^27) the plan takes the
+    # split-K MFMA-tile kernel instead, which asks for a workspace
+    with pytest.raises(ValueError, match="workspace"):
+        _native.call("cubic_gemm", 16, 1 << 27, 16, 16, 1, 4096, 1 << 27, 8, 128, 0, 16, 4096, None, 0, None)
+    with pytest.raises(ValueError, match="row stride"):   # small-row kernel, 32-bit activation extent
+        _native.call("cubic_gemm", 16, 1 << 28, 16, 16, 4, 4096, 4096, 4, 128, 0, 16, 4096, None, 0, None)
     with pytest.raises(ValueError, match="int32 or int64"):
         _native.call("cubic_embedding", 16, 2, 4, 0, 16, 16, 16, 16, None, None, None, None,
                      64, 128, 4, 32, 1, 16, 0, None)

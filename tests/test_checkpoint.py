@@ -244,3 +244,34 @@ def test_sharded_index(tmp_path):
     assert same_payload(plan.materialize(plan.weight("a.proj.weight")), a)
     assert same_payload(plan.materialize(plan.weight("b.proj.weight")), b)
     assert plan.weight("b.proj.weight").encoding.bits == 2
+
+
+def test_declaration_digest_is_blake2s_of_canonical_json():
+    # "b2s256:" + BLAKE2s-256 of the declaration as sorted, compact JSON
+    # (models/quantization.py:117-119); the hex below was computed with
+    # `openssl dgst -blake2s256` over that JSON text, independently of hashlib
+    cfg = ck.QuantizationConfig.from_model_config(config({"g": {"targets": ["lm_head"], "weights": cubic_group(4)}}))
+    assert cfg.digest == "b2s256:3789becc33d6ca0037fe3c09566b8a90b4d9c3f49c4155318799376a7ec44ff8"
+    # key order in the file does not change the identity
+    raw = config({"g": {"targets": ["lm_head"], "weights": cubic_group(4)}})
+    shuffled = {"quantization_config": dict(reversed(list(raw["quantization_config"].items())))}
+    assert ck.QuantizationConfig.from_model_config(shuffled).digest == cfg.digest
+
+
+def test_text_config_prefix_rewrite_follows_the_module():
+    # models/quantization.py:131-136: a text_config declaration rewrites every
+    # name (aliases too) only when the module itself sits under
+    # model.language_model.; otherwise no name is rewritten
+    nested = ck.QuantizationConfig.from_model_config(
+        {"text_config": config({"g": {"targets": ["model.layers.0.mlp.up_proj"], "weights": cubic_group(4)}})})
+    assert nested.resolve("model.language_model.layers.0.mlp.up_proj").bits == 4
+    # wrapped module, wrapped alias: both rewritten, the alias matches
+    assert nested.resolve("model.language_model.layers.0.mlp.gate_up",
+                          aliases=("model.language_model.layers.0.mlp.up_proj",)).bits == 4
+    # unwrapped module: its wrapped alias keeps the prefix and matches nothing
+    assert nested.resolve("model.layers.1.mlp.gate_up",
+                          aliases=("model.language_model.layers.0.mlp.up_proj",)) is None
+    # a root declaration never rewrites
+    root = ck.QuantizationConfig.from_model_config(
+        config({"g": {"targets": ["model.layers.0.mlp.up_proj"], "weights": cubic_group(4)}}))
+    assert root.resolve("model.language_model.layers.0.mlp.up_proj") is None
