@@ -5,6 +5,8 @@
 //   decode       quantization/extensions/cubic/reference.py:98-121
 //   WNA16 linear ops/eager/quantization.py:181-186, ops/eager/linear.py:43-56
 //   dispatch     quantization/extensions/cubic/marlin.py:377-521 (Marlin + merge)
+#include <type_traits>
+
 #include "cubic_gemm_common.h"
 
 namespace cubic {
@@ -44,6 +46,19 @@ using namespace gemm;
 // has landed, while the S - 2 younger groups stay in flight.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
+// f(integral_constant<I>) for I = B .. E - 1, unrolled at compile time
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+// s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters
+// alone (gfx9 layout: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at
+// [15:14]).  Issued through the builtin rather than inline assembly, the
+// compiler's own wait insertion knows which loads it has retired.
+constexpr int vmcnt_only(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
 template <int BITS, int MT, int J, bool TL, int S, int WV, bool F16>
 __global__ __launch_bounds__(WV * 64) void panel_kernel(GemmArgs a) {
     static_assert(BITS <= 4, "level-table decode only");
@@ -213,19 +228,16 @@ __global__ __launch_bounds__(WV * 64) void panel_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     TL_STAMP(2);
 
-    for (int i0 = 0; i0 < n_iter; i0 += S) {
-#pragma unroll
-        for (int st = 0; st < S; ++st) {
-            // a partial last round (the count is even, not a multiple of S);
-            // every wave of the block takes the same exit
-            if (i0 + st >= n_iter) break;
-            const int kb = kb_begin + i0 + st;
+    // one k-block: `st` is its ring stage (compile time), `it` its index
+    auto iteration = [&](auto st_c, int it) {
+            constexpr int st = decltype(st_c)::value;
+            const int kb = kb_begin + it;
             // this wave's group for k-block kb has landed (the S - 2 younger
             // groups may still be in flight); after the barrier every wave's
             // has, and every wave is done with k-block kb - 1's stage
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((S - 2) * kGroupOps) : "memory");
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * kGroupOps));
+            __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            const int it = i0 + st;
             if (it < 19) TL_STAMP(3 + 3 * it);
             // the group for k-block kb + S - 1 goes into the stage and ring
             // slot that the barrier just freed, ahead of this block's math
@@ -274,6 +286,18 @@ __global__ __launch_bounds__(WV * 64) void panel_kernel(GemmArgs a) {
             __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             if (it < 19) TL_STAMP(5 + 3 * it);
+    };
+    // whole rounds of S k-blocks, then (S = 4, an even count that is not a
+    // multiple of 4) the last two.  The tail stays outside the loop: a
+    // conditional exit inside the round makes the compiler drain every load
+    // at the loop head, the S - 2 groups in flight included.
+    const int whole = n_iter - n_iter % S;
+    for (int i0 = 0; i0 < whole; i0 += S)
+        static_for<0, S>([&](auto st_c) { iteration(st_c, i0 + decltype(st_c)::value); });
+    if constexpr (S == 4) {
+        if (whole < n_iter) {
+            iteration(std::integral_constant<int, 0>{}, whole);
+            iteration(std::integral_constant<int, 1>{}, whole + 1);
         }
     }
     TL_STAMP(60);
@@ -299,6 +323,9 @@ hipError_t launch_panel_tl(const GemmArgs& a, dim3 grid, hipStream_t s) {
 }
 template <int BITS, int MT, int J, int S, bool F16>
 hipError_t launch_panel_w(const GemmArgs& a, dim3 grid, hipStream_t s) {
+#ifdef CUBIC_EXPERIMENTS
+    if (a.panel_waves == 8) return launch_panel_tl<BITS, MT, J, S, 8, F16>(a, grid, s);
+#endif
     if (a.panel_waves != kGemmWaves) return hipErrorInvalidValue;
     return launch_panel_tl<BITS, MT, J, S, kGemmWaves, F16>(a, grid, s);
 }
@@ -312,6 +339,10 @@ hipError_t launch_panel_j(const GemmArgs& a, dim3 grid, hipStream_t s) {
     switch (a.tiles_per_wave) {
         case 1: return launch_panel_s<BITS, MT, 1, F16>(a, grid, s);
         case 2: return launch_panel_s<BITS, MT, 2, F16>(a, grid, s);
+#ifdef CUBIC_EXPERIMENTS
+        case 3: return launch_panel_s<BITS, MT, 3, F16>(a, grid, s);
+        case 4: return launch_panel_s<BITS, MT, 4, F16>(a, grid, s);
+#endif
         default: return hipErrorInvalidValue;
     }
 }
@@ -330,6 +361,11 @@ hipError_t launch_panel_bits(const GemmArgs& a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_panel_gemm(const GemmArgs& a, hipStream_t s) {
+#ifdef CUBIC_EXP_FAST
+    if (a.bits != 4 || a.f16 || a.m < 33) return hipErrorInvalidValue;
+    const int cols = a.panel_waves * a.tiles_per_wave * 16;
+    return launch_panel_j<4, 4, false>(a, dim3((a.n + cols - 1) / cols, a.split, 1), s);
+#endif
     switch (a.bits) {
         case 1: return launch_panel_bits<1>(a, s);
         case 2: return launch_panel_bits<2>(a, s);
