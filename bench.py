@@ -219,6 +219,25 @@ def time_graph(graph, reps: int, warmup: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def stream_floor_ms(nbytes: int) -> float:
+    """Measured stream floor at one kernel's size: the time of torch's
+    elementwise copy moving `nbytes` HBM bytes (half read, half written), over
+    distinct buffers totalling >= 2 GB (past the 256 MB Infinity Cache), graph
+    replayed.  It includes the launch ramp a kernel of that size pays, so
+    floor_frac = floor / kernel time is the kernel's share of what a plain
+    stream of its bytes achieves at its size."""
+    import torch
+
+    elems = max(nbytes // 4, 1)  # bf16 elements per side
+    reps = max(2, int(2e9 // max(nbytes, 1)))
+    srcs = [torch.ones(elems, dtype=torch.bfloat16, device="cuda") for _ in range(reps)]
+    dsts = [torch.empty_like(t) for t in srcs]
+    ms = time_graph(capture(lambda: [d.copy_(t) for t, d in zip(srcs, dsts)]), 5, 2) / reps
+    del srcs, dsts
+    torch.cuda.empty_cache()
+    return ms
+
+
 def time_eager(fn, reps: int, warmup: int) -> float:
     """Average ms per launch of back-to-back launches, HIP events recorded on
     the stream the launches go to (torch's current stream)."""
@@ -675,8 +694,10 @@ def main(argv=None) -> int:
     # fused acceptance (HIP events on the stream the launches run on)
     per_ms = time_linears(step, args.layers)
     per_ms["lm_head"] = time_graph(capture(step["lm_binding"].launch), 50, 5)
-    acc_graph = capture(lambda: step["plan"].launch())
-    acc_ms = time_graph(acc_graph, 200, 10)
+    # 20 launches per graph (as the layer linears are timed): the per-replay
+    # graph launch gap is not part of the acceptance's cost inside the step
+    acc_graph = capture(lambda: [step["plan"].launch() for _ in range(20)])
+    acc_ms = time_graph(acc_graph, 20, 3) / 20
 
     nb = step_bytes(args.layers)
     value = nb["total"] / (ms_per_step * 1e-3) / 1e9
@@ -687,8 +708,10 @@ def main(argv=None) -> int:
         launches = args.layers if name in shapes else 1
         byts = gemm_bytes(M_ROWS, n, k)
         gbs = byts / (ms * 1e-3) / 1e9
+        floor_ms = stream_floor_ms(byts)
         kernels[name] = {"us": round(ms * 1e3, 2), "bytes_per_launch": byts, "gbs": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "floor_us": round(floor_ms * 1e3, 2), "floor_frac": round(floor_ms / ms, 4),
                          "share_of_step": round(launches * ms / ms_per_step, 4)}
     dominant = max(kernels, key=lambda k: kernels[k]["share_of_step"])
     traffic = {}
