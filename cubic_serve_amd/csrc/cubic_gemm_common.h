@@ -308,6 +308,38 @@ __device__ __forceinline__ void reduce_partials(__amdgpu_buffer_rsrc_t part, int
     }
 }
 
+// Second arrival of a two-partition output block: each thread adds the two
+// partitions of the units it computed itself (its J x MT accumulators), in K
+// order, reading the first arrival's partials from the workspace and taking
+// its own partition `mine` from its registers.
+template <int J, int MT, bool F16, int WV = kGemmWaves>
+__device__ __forceinline__ void reduce_pair(__amdgpu_buffer_rsrc_t part, int split_bytes, int mine,
+                                            const floatx4_t (&acc)[MT][J], uint16_t* tile, int wave, int lane) {
+    constexpr int kPer = J * MT;
+    constexpr int kBatch = largest_divisor_at_most(kPer, 8);
+    constexpr int P = tile_pitch<J, WV>();
+    const int q = lane >> 4, col = lane & 15;
+    const int other = (1 - mine) * split_bytes;
+#pragma unroll
+    for (int b0 = 0; b0 < kPer; b0 += kBatch) {
+        floatx4_dev_t v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int u = b0 + b, j = u / MT, mt = u % MT;
+            v[b] = load_device4(part, other + (((wave * J + j) * MT + mt) * kWave + lane) * 16);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int u = b0 + b, j = u / MT, mt = u % MT;
+            const floatx4_dev_t own = acc[mt][j];
+            const floatx4_dev_t sum = mine == 0 ? own + v[b] : v[b] + own;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                tile[(mt * 16 + 4 * q + r) * P + (wave * J + j) * 16 + col] = out_bits<F16>(sum[r]);
+        }
+    }
+}
+
 // Output of one block: split = 1 stores bf16 through the LDS tile; a K split
 // stores the FP32 accumulators in the MFMA-native layout (one 16-byte unit per
 // tile, m-tile and lane) and the last arrival sums the K partitions in
@@ -336,22 +368,59 @@ __device__ __forceinline__ void finish_block(const GemmArgs& a, const floatx4_t 
     const int split_bytes = (int)(gridDim.x * gridDim.z) * kUnits * 16;  // < 2^31: split > 1 only below 256 blocks of <= 64 KiB
     const __amdgpu_buffer_rsrc_t part =
         device_rsrc(reinterpret_cast<char*>(a.partials) + (int64_t)block * kUnits * 16);
+    const auto store_partials = [&]() {
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            store_device4(part, blockIdx.y * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
-                          acc[mt][j]);
-    __shared__ uint32_t last;
-    if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
-    switch (a.split) {  // arrive_last's barriers leave the tile free
-        case 2: reduce_partials<2, J, MT, F16, WV>(part, split_bytes, tile); break;
-        case 3: reduce_partials<3, J, MT, F16, WV>(part, split_bytes, tile); break;
-        case 4: reduce_partials<4, J, MT, F16, WV>(part, split_bytes, tile); break;
-        case 5: reduce_partials<5, J, MT, F16, WV>(part, split_bytes, tile); break;
-        case 6: reduce_partials<6, J, MT, F16, WV>(part, split_bytes, tile); break;
-        case 7: reduce_partials<7, J, MT, F16, WV>(part, split_bytes, tile); break;
-        default: reduce_partials<8, J, MT, F16, WV>(part, split_bytes, tile); break;
+            for (int mt = 0; mt < MT; ++mt)
+                store_device4(part, blockIdx.y * split_bytes + (((wave * J + j) * MT + mt) * kWave + lane) * 16,
+                              acc[mt][j]);
+    };
+    if (a.split == 2) {
+        // Two partitions: the block's counter word counts arrivals in its low
+        // half and stored partitions in its high half.  A workgroup takes its
+        // arrival ticket first; the first stores its FP32 partials (device-
+        // scope stores, performed before the count goes up) and counts
+        // itself stored; the second never stores: it waits until the first
+        // is stored and sums both in K order, its own from registers.  (With
+        // more partitions the last arrival waits on the slowest of several
+        // partners' ticket-then-store sequences, which measured slower than
+        // storing first.)
+        __shared__ uint32_t ticket;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            ticket = __hip_atomic_fetch_add(&a.counters[block], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                     0xFFFFu;
+        __syncthreads();
+        if (ticket == 0) {
+            store_partials();
+            __builtin_amdgcn_s_waitcnt(0);  // this thread's partials are performed
+            __syncthreads();
+            if (threadIdx.x == 0)
+                __hip_atomic_fetch_add(&a.counters[block], 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        if (threadIdx.x == 0) {
+            // the first has taken its ticket, so it is running and only has
+            // its stores left; the bound only keeps a broken workspace (a
+            // counter not zero at launch) from spinning forever
+            for (int spin = 0; spin < (1 << 24) && (load_device(&a.counters[block]) >> 16) == 0u; ++spin)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        __syncthreads();
+        reduce_pair<J, MT, F16, WV>(part, split_bytes, (int)blockIdx.y, acc, tile, wave, lane);
+    } else {
+        store_partials();
+        __shared__ uint32_t last;
+        if (!arrive_last(&a.counters[block], (uint32_t)a.split, &last)) return;
+        switch (a.split) {  // arrive_last's barriers leave the tile free
+            case 3: reduce_partials<3, J, MT, F16, WV>(part, split_bytes, tile); break;
+            case 4: reduce_partials<4, J, MT, F16, WV>(part, split_bytes, tile); break;
+            case 5: reduce_partials<5, J, MT, F16, WV>(part, split_bytes, tile); break;
+            case 6: reduce_partials<6, J, MT, F16, WV>(part, split_bytes, tile); break;
+            case 7: reduce_partials<7, J, MT, F16, WV>(part, split_bytes, tile); break;
+            default: reduce_partials<8, J, MT, F16, WV>(part, split_bytes, tile); break;
+        }
     }
     if (threadIdx.x == 0) store_device(&a.counters[block], 0u);
     __syncthreads();
