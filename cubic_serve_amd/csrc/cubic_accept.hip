@@ -961,9 +961,52 @@ __device__ bool tile_top(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx
 // composite (value desc, then lowest id; the composite order of tile_top) in
 // out_top[0] and zeros in the other slots.  Returns the non-finite flag as
 // tile_top does.
+// Whole tiles (every element of the lane's EMAX chunks exists): one pass of
+// six VALU per word.  Prefilter keys (prefilter_key2) order like the values
+// except that -0 sits just below +0, which the exact order ties; the lane's
+// composite is (prefilter key << 16 | last - local position), its maximum the
+// largest key at the lowest position, found with a three-input maximum per
+// word.  A wave whose maximum key is -0 or +0 (the one place the two orders
+// differ) returns false and takes the general path; otherwise out_top[0] is
+// the exact composite tile_max_general computes.  *nonfinite: as tile_top.
+template <int EMAX, bool HALF>
+__device__ bool tile_max_whole(const uint4 (&raw)[EMAX], uint32_t base_idx, int lane, uint32_t* out_top,
+                               bool* nonfinite) {
+    constexpr uint32_t kLast = EMAX * 8 - 1;  // the lane's last position
+    uint32_t best = 0;
+    u16x2_t kmin = {0xFFFF, 0xFFFF};
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t k2 = prefilter_key2((&raw[e].x)[w]);
+            kmin = __builtin_elementwise_min(kmin, __builtin_bit_cast(u16x2_t, k2));
+            const uint32_t pos = (uint32_t)(e * 8 + 2 * w);  // lane-local position of the low half
+            const uint32_t c_lo = (k2 << 16) | (kLast - pos);
+            const uint32_t c_hi = (k2 & 0xFFFF0000u) | (kLast - 1u - pos);
+            const uint32_t m = c_lo > c_hi ? c_lo : c_hi;
+            best = m > best ? m : best;
+        }
+    const uint32_t key = best >> 16, pos = kLast - (best & 0xFFFFu);
+    constexpr uint32_t kHi = HALF ? 0xFC00u : 0xFF80u, kLo = HALF ? 0x03FFu : 0x007Fu;
+    *nonfinite = key >= kHi || kmin.x <= kLo || kmin.y <= kLo;
+    const uint32_t wave_key = wave_max_u32(key);
+    if (wave_key == 0x7FFFu || wave_key == 0x8000u) return false;  // wave-uniform
+    // position (chunk e, element j of the lane's 8) -> tile index
+    const uint32_t idx = base_idx + (pos >> 3) * kChunk + (pos & 7u);
+    uint32_t lane_best = (exact_of_prefilter(key) << 16) | (0xFFFFu - idx);
+    lane_best = wave_max_u32(lane_best);
+    if (lane < kTop) out_top[lane] = lane == 0 ? lane_best : 0u;
+    return true;
+}
+
 template <int EMAX, bool HALF>
 __device__ bool tile_max(const uint4 (&raw)[EMAX], int chunks, uint32_t base_idx, int width_left,
                          int lane, uint32_t* out_top) {
+    if (chunks == EMAX && chunks * kChunk <= width_left) {  // wave-uniform
+        bool nonfinite = false;
+        if (tile_max_whole<EMAX, HALF>(raw, base_idx, lane, out_top, &nonfinite)) return nonfinite;
+    }
     // Per word (two elements): packed order keys, masked to 0 (empty) past the
     // tile; the word's larger key and the word's position form a composite
     // whose maximum is the lane's largest key in its lowest word; inside that

@@ -57,6 +57,15 @@ def test_candidates_match_oracle(oracle, rows, width):
         bits[4] = bits[4] | np.uint16(0x8000)
         bits[4, 100] = np.uint16(0x8000)
         bits[4, width - 5] = np.uint16(0x0000)
+    if rows > 16:
+        # greedy rows 7, 10, 13, 16 inside whole tiles (8 chunks of 2048, a
+        # lane holding elements 8 l .. 8 l + 7 of each chunk): a maximum tied
+        # within one lane across chunks, within one 32-bit word, at a lane's
+        # last element, and a -inf (non-finite row)
+        bits[7, 3] = bits[7, 3 + 2048] = np.uint16(0x4400)
+        bits[10, 4] = bits[10, 5] = np.uint16(0x4400)
+        bits[13, 40 + 7 * 2048 + 7] = np.uint16(0x4400)
+        bits[16, 1000] = np.uint16(0xFF80)
     temps = np.array([(0.0 if r % 3 == 1 else 0.7) for r in range(rows)], np.float32)
     owned = max(1, rows - 1)
     count, capacity = 20, 24
@@ -91,6 +100,15 @@ def test_fp16_candidates_match_oracle(oracle, rows, width):
         bits[4] = bits[4] | np.uint16(0x8000)             # greedy row, all negative but -0/+0
         bits[4, 100] = np.uint16(0x8000)
         bits[4, width - 5] = np.uint16(0x0000)
+    if rows > 16:
+        # greedy rows 7, 10, 13, 16 inside whole tiles (8 chunks of 2048, a
+        # lane holding elements 8 l .. 8 l + 7 of each chunk): a maximum tied
+        # within one lane across chunks, within one 32-bit word, at a lane's
+        # last element, and a -inf (non-finite row)
+        bits[7, 3] = bits[7, 3 + 2048] = np.uint16(0x4400)
+        bits[10, 4] = bits[10, 5] = np.uint16(0x4400)
+        bits[13, 40 + 7 * 2048 + 7] = np.uint16(0x4400)
+        bits[16, 1000] = np.uint16(0xFF80)
     temps = np.array([(0.0 if r % 3 == 1 else 0.7) for r in range(rows)], np.float32)
     count, capacity = 20, 24
     scores = torch.empty((rows, capacity), dtype=torch.float16, device=DEV)
