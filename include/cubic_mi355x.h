@@ -95,7 +95,10 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  * The regimes, as the reference's: m <= 4 with groups of whole 128-wide
  * k-blocks runs the small-row kernel (bits <= 4 at any k; 5..8 bits while k
  * is at most 64 k-blocks), one partition per wave, a function of k alone;
- * every other m runs the MFMA-tile kernel with the K plan above.
+ * every other m runs the MFMA-tile arithmetic with the K plan above (m <= 64
+ * at bits <= 4 on column panels that share each staged activation block over
+ * several tiles, the rest one tile per wave; both issue the same MFMA
+ * sequence and agree bit for bit).
  *
  * cubic_gemm_workspace_bytes: workspace for (m, n, k); 0 when no K split.
  *   The workspace must be zero-filled before its first use; every completed
