@@ -90,16 +90,20 @@ bool small_rows(int64_t m, int bits, int group_in, int64_t k) {
 }
 
 // K partition of one member: split in powers of two (at most 8) until a
-// partition holds at most 16 k-blocks and about 256 workgroups of one tile
-// per wave are in flight; a member wide enough to fill the GPU with two tiles
-// per wave keeps K whole.
+// partition holds at most 16 k-blocks -- 32 when the unsplit member already
+// gives >= 384 workgroups of one tile per wave -- and about 256 workgroups of
+// one tile per wave are in flight; a member wide enough to fill the GPU with
+// two tiles per wave keeps K whole.  (The 32-block cap: Llama-3-70B gate/up
+// members, 28672 x 8192, split 2 instead of 4: grouped launch 607 -> 521 us
+// at M = 512, 61 -> 57 at M = 8, equal at M = 64, same box.)
 void plan_k(int64_t n_member, int64_t k, int* split_out, int* bps_out) {
     const int64_t tiles = ceil_div(n_member, 16);
     const int k_blocks = (int)ceil_div(k, kKBlock);
     int split = 1;
     if (ceil_div(tiles, 2 * cubic::kGemmWaves) < 256) {
         const int64_t out_blocks = ceil_div(tiles, cubic::kGemmWaves);
-        while (split < 8 && (ceil_div(k_blocks, split) > 16 || out_blocks * split < 256)) split *= 2;
+        const int kb_cap = out_blocks >= 384 ? 32 : 16;
+        while (split < 8 && (ceil_div(k_blocks, split) > kb_cap || out_blocks * split < 256)) split *= 2;
         if (split > k_blocks / 2) split = k_blocks / 2 > 0 ? k_blocks / 2 : 1;
     }
     const int bps = (int)ceil_div(k_blocks, split);
