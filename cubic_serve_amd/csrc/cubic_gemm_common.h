@@ -243,6 +243,28 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* ti
     constexpr int kSegs = C / 8, kChunks = 16 * MT * kSegs;
     const int n_base = blockIdx.x * C;
     const int rows = a.routed ? a.routes : a.m;
+    // Whole block inside one member, in range and 16-byte aligned in every
+    // row: the member, its pointer and its row stride are block-uniform
+    // (scalar registers), and every segment is one 16-byte store.
+    const int member0 = n_base / a.n_member;
+    const int nl0 = n_base - member0 * a.n_member;
+    if (n_base + C <= a.n && nl0 + C <= a.n_member) {
+        uint16_t* y0 = a.ys[member0] + nl0;
+        const int64_t ldy = a.ldys[member0];
+        if (((reinterpret_cast<uintptr_t>(y0) | (uintptr_t)ldy * 2) & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < (kChunks + kThr - 1) / kThr; ++i) {
+                const int c = threadIdx.x + kThr * i;
+                if (c >= kChunks) break;
+                const int row = c / kSegs, seg = c % kSegs;
+                const int m = a.routed ? a.padded[m0 + row] : m0 + row;
+                if (m >= rows) continue;
+                *reinterpret_cast<uint4*>(y0 + (int64_t)m * ldy + seg * 8) =
+                    *reinterpret_cast<const uint4*>(&tile[row * P + seg * 8]);
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < (kChunks + kThr - 1) / kThr; ++i) {
         const int c = threadIdx.x + kThr * i;
