@@ -1355,6 +1355,153 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(AcceptArgs a) {
     }
 }
 
+// --------------------------------------------------------------------------
+// fp32 candidate preparation (local_candidates.py:41 SCORE_TYPE 2, kernels
+// local_candidates.cu:19-146).  Same rules as the 16-bit path: order by value
+// (-0 == +0), ties by ascending column, raw scores published, -2 in every
+// counted slot of a row with a non-finite logit, greedy rows publish the
+// argmax in slot 0 (padding when all_random).  A 64-bit composite carries the
+// order key of the value above 0xFFFFFFFF - column, so the larger composite
+// is the better candidate and every composite of a real column is nonzero.
+// --------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t f32_composite(uint32_t u, uint32_t col) {
+    const uint32_t m = u & 0x7FFFFFFFu;
+    const uint32_t key = (u & 0x80000000u) ? 0x80000000u - m : 0x80000000u + m;
+    return ((uint64_t)key << 32) | (0xFFFFFFFFu - col);
+}
+
+__device__ __forceinline__ bool f32_row_owned(const CandF32Args& a, int row) {
+    int owned = a.owned_rows;
+    if (a.owned_count) {
+        const int v = a.owned_count[0];
+        owned = v < 0 ? 0 : (v > a.rows ? a.rows : v);
+    }
+    return row < owned && (!a.row_activity || a.row_activity[row] != 0);
+}
+
+__device__ __forceinline__ int f32_want(const CandF32Args& a, int row) {
+    return a.row_temperatures[row] == 0.0f ? 1 : a.count;
+}
+
+constexpr int kF32Waves = kThreads / kWave;
+constexpr int kF32WaveCols = kCandF32Tile / kF32Waves;  // 1024
+constexpr int kF32PerLane = kF32WaveCols / kWave;       // 16
+
+// Workgroup (tile, row): the top `want` composites of kCandF32Tile columns
+// and whether all of them are finite.  Wave w reads columns
+// [w * 1024, (w + 1) * 1024) of the tile: 16-byte loads of four columns per
+// lane per round when the rows are 16-byte aligned, else one column per lane.
+__global__ __launch_bounds__(kThreads) void cand_f32_tile_kernel(CandF32Args a) {
+    __shared__ uint64_t buf[kF32Waves][kWave];
+    __shared__ uint64_t wave_top[kF32Waves * kTop];
+    __shared__ uint32_t wave_good[kF32Waves];
+    const int tile = blockIdx.x, row = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (!f32_row_owned(a, row)) return;  // published as padding; partials unread
+    const int want = f32_want(a, row);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.logits) + (int64_t)row * a.row_stride;
+    const int c0 = tile * kCandF32Tile + wave * kF32WaveCols;
+    uint64_t e[kF32PerLane];
+    uint32_t bad = 0;
+    if (a.vector_loads) {
+#pragma unroll
+        for (int q = 0; q < kF32PerLane / 4; ++q) {
+            const int c = c0 + q * 4 * kWave + lane * 4;
+            uint32_t u[4];
+            if (c + 4 <= a.width) {
+                const uint4 v = *reinterpret_cast<const uint4*>(src + c);
+                u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) u[i] = c + i < a.width ? src[c + i] : 0u;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool in = c + i < a.width;
+                bad |= in && (u[i] & 0x7F800000u) == 0x7F800000u;
+                e[q * 4 + i] = in ? f32_composite(u[i], (uint32_t)(c + i)) : 0ull;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kF32PerLane; ++q) {
+            const int c = c0 + q * kWave + lane;
+            const bool in = c < a.width;
+            const uint32_t u = in ? src[c] : 0u;
+            bad |= in && (u & 0x7F800000u) == 0x7F800000u;
+            e[q] = in ? f32_composite(u, (uint32_t)c) : 0ull;
+        }
+    }
+    const uint64_t top = wave_topk_u64<kF32PerLane>(e, kF32WaveCols, want, lane, buf[wave]);
+    if (lane < want) wave_top[wave * kTop + lane] = top;
+    const bool wave_bad = __any(bad);
+    if (lane == 0) wave_good[wave] = !wave_bad;
+    __syncthreads();
+    if (wave != 0) return;
+    uint64_t m[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = lane + h * kWave, w = i / kTop, r = i % kTop;
+        m[h] = (w < kF32Waves && r < want) ? wave_top[i] : 0ull;
+    }
+    const uint64_t best = wave_topk_u64<2>(m, 2 * kWave, want, lane, buf[0]);
+    const int64_t slot = (int64_t)row * a.tiles + tile;
+    if (lane < want) a.partial[slot * kTop + lane] = best;
+    if (lane == 0) {
+        uint32_t g = 1;
+#pragma unroll
+        for (int w = 0; w < kF32Waves; ++w) g &= wave_good[w];
+        a.partial_finite[slot] = g;
+    }
+}
+
+// One wave per row: merges the tiles' lists (7 * 64 entries per round, the
+// running top carried in the first entry of each lane) and publishes.
+__global__ __launch_bounds__(kWave) void cand_f32_publish_kernel(CandF32Args a) {
+    __shared__ uint64_t buf[kWave];
+    constexpr int kP = 8;
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const bool owned = f32_row_owned(a, row);
+    const bool greedy = a.row_temperatures[row] == 0.0f;
+    const int want = f32_want(a, row);
+    uint32_t good = 1;
+    uint64_t run = 0;
+    if (owned) {
+        for (int t = lane; t < a.tiles; t += kWave) good &= a.partial_finite[(int64_t)row * a.tiles + t];
+        good = !__any(!good);
+        if (good) {
+            const int n = a.tiles * want;
+            for (int base = 0; base < n; base += (kP - 1) * kWave) {
+                uint64_t e[kP];
+                e[0] = lane < want ? run : 0ull;
+#pragma unroll
+                for (int q = 1; q < kP; ++q) {
+                    const int i = base + (q - 1) * kWave + lane;
+                    e[q] = i < n ? a.partial[((int64_t)row * a.tiles + i / want) * kTop + i % want] : 0ull;
+                }
+                run = wave_topk_u64<kP>(e, kP * kWave, want, lane, buf);
+            }
+        }
+    }
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.logits) + (int64_t)row * a.row_stride;
+    // capacity <= 64: lane j publishes slot j, and holds rank j of `run`
+    if (lane < a.capacity) {
+        uint32_t score = 0x7FC00000u;
+        int64_t id = -1;
+        if (owned && lane < a.count) {
+            if (!good) {
+                id = -2;
+            } else if ((!greedy || (!a.all_random && lane == 0)) && run != 0ull) {
+                const uint32_t col = 0xFFFFFFFFu - (uint32_t)run;
+                score = src[col];
+                id = a.vocab_start + col;
+            }
+        }
+        reinterpret_cast<uint32_t*>(a.scores)[(int64_t)row * a.capacity + lane] = score;
+        a.ids[(int64_t)row * a.capacity + lane] = id;
+    }
+}
+
 template <int EMAX, bool FUSED>
 hipError_t launch_accept_slots(const AcceptArgs& a, hipStream_t s) {
     dim3 grid(a.tiles, a.rows), block(kThreads);
@@ -1381,6 +1528,15 @@ hipError_t launch_accept(const AcceptArgs& a, bool fused, hipStream_t s) {
     if (chunks <= kMaxTileChunks)
         return fused ? launch_accept_slots<16, true>(a, s) : launch_accept_slots<16, false>(a, s);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_candidates_f32(const CandF32Args& a, hipStream_t s) {
+    if (a.count < 1 || a.count > kTop || a.capacity < a.count || a.capacity > kWave) return hipErrorInvalidValue;
+    cand_f32_tile_kernel<<<dim3(a.tiles, a.rows), kThreads, 0, s>>>(a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    cand_f32_publish_kernel<<<a.rows, kWave, 0, s>>>(a);
+    return hipGetLastError();
 }
 
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t s) {

@@ -676,8 +676,17 @@ int cubic_moe_gemm(const void* x, int64_t ldx, const uint32_t* codes, const uint
 }
 
 
+// fp32 logits: [rows, tiles, 20] composite keys + [rows, tiles] finite flags
+int64_t cand_f32_workspace(int rows, int width) {
+    if (rows <= 0 || width <= 0) return -1;
+    const int64_t tiles = ceil_div(width, cubic::kCandF32Tile);
+    return align256((int64_t)rows * tiles * kTop * 8) + align256((int64_t)rows * tiles * 4);
+}
+
 int64_t cubic_candidates_workspace_bytes(int rows, int width) {
-    return accept_workspace(rows, rows, width);
+    // one size for every logits dtype: the larger of the two plans
+    const int64_t a16 = accept_workspace(rows, rows, width), a32 = cand_f32_workspace(rows, width);
+    return a16 > a32 ? a16 : a32;
 }
 
 int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows, int width,
@@ -686,13 +695,39 @@ int cubic_candidates(const void* logits, int dtype, int64_t row_stride, int rows
                      int all_random, void* scores, int64_t* ids, void* workspace,
                      int64_t workspace_bytes, void* stream) {
     if (!logits || !temperatures || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "null operand");
-    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16)
-        return fail(CUBIC_EINVAL, "candidate logits dtype must be CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16");
+    if (dtype != CUBIC_DTYPE_BF16 && dtype != CUBIC_DTYPE_F16 && dtype != CUBIC_DTYPE_F32)
+        return fail(CUBIC_EINVAL, "candidate logits dtype must be CUBIC_DTYPE_BF16, _F16 or _F32");
     if (vocab_start < 0) return fail(CUBIC_EINVAL, "negative vocabulary start");
     if (rows <= 0 || width <= 0 || row_stride < width) return fail(CUBIC_EINVAL, "invalid logits geometry");
     if (owned_rows < 0 || owned_rows > rows) return fail(CUBIC_EINVAL, "owned_rows outside 0..rows");
     if (count < 1 || count > kTop || capacity < count || capacity > 64)
         return fail(CUBIC_EINVAL, "need 1 <= count <= 20 and count <= capacity <= 64");
+    if (dtype == CUBIC_DTYPE_F32) {
+        const int64_t need = cand_f32_workspace(rows, width);
+        if (workspace_bytes < need)
+            return fail(CUBIC_EWORKSPACE, "candidate workspace %lld < %lld", (long long)workspace_bytes, (long long)need);
+        const int64_t tiles = ceil_div(width, cubic::kCandF32Tile);
+        cubic::CandF32Args f = {};
+        f.logits = (const float*)logits;
+        f.row_stride = row_stride;
+        f.rows = rows;
+        f.width = width;
+        f.tiles = (int)tiles;
+        f.vector_loads = aligned16(logits) && row_stride % 4 == 0;
+        f.row_temperatures = temperatures;
+        f.owned_rows = owned_rows;
+        f.count = count;
+        f.capacity = capacity;
+        f.all_random = all_random;
+        f.vocab_start = vocab_start;
+        f.owned_count = owned_count;
+        f.row_activity = row_activity;
+        f.scores = (float*)scores;
+        f.ids = ids;
+        f.partial = (uint64_t*)workspace;
+        f.partial_finite = (uint32_t*)((char*)workspace + align256((int64_t)rows * tiles * kTop * 8));
+        return hip_status(cubic::launch_candidates_f32(f, (hipStream_t)stream), "cubic_candidates launch");
+    }
     TilePlan t;
     if (!plan_tiles(rows, width, &t)) return fail(CUBIC_ENOTSUP, "vocabulary width %d too large", width);
     const int64_t need = accept_workspace(rows, rows, width);

@@ -52,6 +52,23 @@ struct AcceptArgs {
     int64_t* emitted;             // [c, depth + 1] or null
 };
 
+// fp32 candidate preparation (SCORE_TYPE 2): a tile pass over (tile, row)
+// workgroups, then one publishing wave per row.
+struct CandF32Args {
+    const float* logits;          // [rows, row_stride]
+    int64_t row_stride;           // elements
+    int rows, width, tiles, vector_loads;
+    const float* row_temperatures;  // [rows]: 0 = greedy publication
+    int owned_rows, count, capacity, all_random;
+    int64_t vocab_start;
+    const int32_t* owned_count;   // device: rows < owned_count[0] are owned, or null
+    const uint8_t* row_activity;  // [rows] or null
+    float* scores;                // [rows, capacity]
+    int64_t* ids;                 // [rows, capacity]
+    uint64_t* partial;            // [rows, tiles, 20] composite keys of each tile's top
+    uint32_t* partial_finite;     // [rows, tiles]
+};
+
 struct VerifyArgs {
     const uint16_t* q_scores;  // [tp, q_rows, k] bf16
     const int64_t* q_ids;
@@ -228,6 +245,8 @@ hipError_t launch_greedy(const GreedyArgs& a, hipStream_t s);
 hipError_t launch_greedy_root(const GreedyRootArgs& a, hipStream_t s);
 hipError_t launch_final_guard(const GuardArgs& a, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t s);
+hipError_t launch_candidates_f32(const CandF32Args& a, hipStream_t s);
+constexpr int kCandF32Tile = 4096;  // columns per fp32 candidate tile
 hipError_t launch_root_sample(const RootSampleArgs& a, hipStream_t s);
 hipError_t launch_merge_prefix(const int64_t* decisions, int c, int depth, const int32_t* live,
                                int live_rows, int64_t* out, hipStream_t s);

@@ -240,21 +240,24 @@ def merge_prefix(decisions: Tensor, out: Tensor, live: Tensor | int) -> None:
                      out.data_ptr(), _native.stream_of(out.device))
 
 
+# logits dtype -> CUBIC_DTYPE_BF16 / _F16 / _F32 (local_candidates.py:41)
+_CANDIDATE_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
 class LocalCandidatePlan:
     """Vocab logits -> published top-k candidates, bound before capture.
 
     One pass over ``local_logits[:active_rows, :visible_width]`` replaces
     torch.topk + candidate_partial + candidate_publish over this rank's
     vocabulary shard; published ids are ``vocab_start`` + column.  Logits and the
-    published scores are bf16 or fp16 (the reference also admits fp32,
-    local_candidates.py:41, which is not admitted here).
+    published scores are bf16, fp16 or fp32 (local_candidates.py:41).
     """
 
     def __init__(self, *, local_logits: Tensor, workspace: ShardedSamplingWorkspace,
                  active_rows: int, visible_width: int, local_count: int, vocab_start: int = 0,
                  owned_rows: int | None = None, all_random_rows: bool = False,
                  row_activity: Tensor | None = None, metadata: Tensor | None = None) -> None:
-        if (local_logits.dtype not in (torch.bfloat16, torch.float16) or local_logits.ndim != 2
+        if (local_logits.dtype not in _CANDIDATE_DTYPES or local_logits.ndim != 2
                 or local_logits.stride(1) != 1
                 or not 0 < active_rows <= local_logits.shape[0]
                 or not 0 < local_count <= visible_width <= local_logits.shape[1]
@@ -306,7 +309,7 @@ class LocalCandidatePlan:
         scores, ids = self.outputs
         with torch.cuda.device(self.logits.device):
             _native.call("cubic_candidates", self.logits.data_ptr(),
-                         int(self.logits.dtype == torch.float16), self.logits.stride(0),
+                         _CANDIDATE_DTYPES[self.logits.dtype], self.logits.stride(0),
                          self.capacity, self.width, self.vocab_start, self.temperatures.data_ptr(),
                          self.owned_rows,
                          _native.ptr(self.metadata), _native.ptr(self.row_activity),

@@ -48,6 +48,7 @@ CUBIC_API const char* cubic_last_error(void);
  * in the same dtype: ops/cuda/linear/quantized.py:348-405). */
 #define CUBIC_DTYPE_BF16 0
 #define CUBIC_DTYPE_F16 1
+#define CUBIC_DTYPE_F32 2  /* candidate preparation logits only */
 
 /* ---------------------------------------------------------------------------
  * Cubic weight preparation (load time).
@@ -325,8 +326,7 @@ CUBIC_API int cubic_moe_compact(const int64_t* route_ids, int routes, int first_
  * 206-226: torch.topk + candidate_partial/candidate_publish,
  * local_candidates.cu:19-146) and the greedy argmax (greedy.cu:14-78).
  *   logits        [rows, row_stride], width <= row_stride visible columns;
- *                 dtype CUBIC_DTYPE_BF16 or CUBIC_DTYPE_F16 (local_candidates.py:41
- *                 also admits fp32, which this library does not)
+ *                 dtype CUBIC_DTYPE_BF16, _F16 or _F32 (local_candidates.py:41)
  *   temperatures  f32 [rows]; 0 = greedy row (slot 0 = argmax, lowest id on ties)
  *   vocab_start   first token of this shard: published ids are vocab_start + column
  *   scores/ids    logits dtype / int64 [rows, capacity]; padding (NaN, -1); rows with a

@@ -297,49 +297,77 @@ static inline int better(float v, int64_t id, float bv, int64_t bid) {
     return v > bv || (v == bv && id < bid);
 }
 
-/* logits and published scores are bf16 (fp16 = 0) or fp16 (fp16 = 1) bits;
-   the reference publishes its SCORE_TYPE (local_candidates.py:41, :188) */
-EXPORT int oracle_candidates_dtype(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,
-                                   const float* temperatures, int64_t owned_rows, int count,
-                                   int capacity, int all_random, int fp16, uint16_t* out_scores,
-                                   int64_t* out_ids) {
-    if (count < 1 || count > capacity || count > 64) return -1;
-    const uint16_t qnan = fp16 ? 0x7e00u : 0x7fc0u;
-#define ORACLE_SCORE(bits) (fp16 ? oracle_half_to_float(bits) : oracle_bf16_to_float(bits))
+/* logits and published scores in the reference's SCORE_TYPE (local_candidates.py:41,
+   :188): kind 0 = bf16 bits, 1 = fp16 bits, 2 = fp32; scores are published unchanged */
+static float candidate_value(const void* logits, int kind, int64_t i, uint32_t* raw) {
+    if (kind == 2) {
+        float v;
+        memcpy(raw, (const uint32_t*)logits + i, 4);
+        memcpy(&v, raw, 4);
+        return v;
+    }
+    const uint16_t b = ((const uint16_t*)logits)[i];
+    *raw = b;
+    return kind ? oracle_half_to_float(b) : oracle_bf16_to_float(b);
+}
+
+static void candidate_store(void* out, int kind, int64_t i, uint32_t raw) {
+    if (kind == 2) ((uint32_t*)out)[i] = raw;
+    else ((uint16_t*)out)[i] = (uint16_t)raw;
+}
+
+static int candidates_kind(const void* logits, int kind, int64_t rows, int64_t width, int64_t stride,
+                           const float* temperatures, int64_t owned_rows, int count, int capacity,
+                           int all_random, void* out_scores, int64_t* out_ids) {
+    if (count < 1 || count > capacity || count > 64 || kind < 0 || kind > 2) return -1;
+    const uint32_t qnan = kind == 2 ? 0x7fc00000u : kind ? 0x7e00u : 0x7fc0u;
     for (int64_t r = 0; r < rows; ++r) {
-        uint16_t* sc = out_scores + r * capacity;
         int64_t* id = out_ids + r * capacity;
-        for (int j = 0; j < capacity; ++j) { sc[j] = qnan; id[j] = -1; }
+        for (int j = 0; j < capacity; ++j) { candidate_store(out_scores, kind, r * capacity + j, qnan); id[j] = -1; }
         if (r >= owned_rows) continue;
-        const uint16_t* row = logits + r * stride;
+        uint32_t raw;
         int good = 1;
         for (int64_t j = 0; j < width; ++j) {
-            float v = ORACLE_SCORE(row[j]);
-            if (!isfinite(v)) { good = 0; break; }
+            if (!isfinite(candidate_value(logits, kind, r * stride + j, &raw))) { good = 0; break; }
         }
         const int greedy = temperatures[r] == 0.0f;
         if (!good) { for (int j = 0; j < count; ++j) id[j] = -2; continue; }
         /* top-count by (value desc, id asc): insertion into a sorted list; its
            slot 0 is the exact argmax with the lowest id on ties */
-        float bv[64]; int64_t bi[64]; uint16_t braw[64]; int filled = 0;
+        float bv[64]; int64_t bi[64]; uint32_t braw[64]; int filled = 0;
         const int want = count;
         for (int64_t j = 0; j < width; ++j) {
-            float v = ORACLE_SCORE(row[j]);
+            const float v = candidate_value(logits, kind, r * stride + j, &raw);
             if (filled == want && !better(v, j, bv[want - 1], bi[want - 1])) continue;
             int pos = filled < want ? filled++ : want - 1;
             while (pos > 0 && better(v, j, bv[pos - 1], bi[pos - 1])) {
                 bv[pos] = bv[pos - 1]; bi[pos] = bi[pos - 1]; braw[pos] = braw[pos - 1]; --pos;
             }
-            bv[pos] = v; bi[pos] = j; braw[pos] = row[j];
+            bv[pos] = v; bi[pos] = j; braw[pos] = raw;
         }
         if (!greedy) {
-            for (int j = 0; j < filled; ++j) { sc[j] = braw[j]; id[j] = bi[j]; }
+            for (int j = 0; j < filled; ++j) { candidate_store(out_scores, kind, r * capacity + j, braw[j]); id[j] = bi[j]; }
         } else if (!all_random && filled) {
-            sc[0] = braw[0]; id[0] = bi[0];
+            candidate_store(out_scores, kind, r * capacity, braw[0]); id[0] = bi[0];
         }
     }
-#undef ORACLE_SCORE
     return 0;
+}
+
+EXPORT int oracle_candidates_dtype(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,
+                                   const float* temperatures, int64_t owned_rows, int count,
+                                   int capacity, int all_random, int fp16, uint16_t* out_scores,
+                                   int64_t* out_ids) {
+    return candidates_kind(logits, fp16 ? 1 : 0, rows, width, stride, temperatures, owned_rows, count,
+                           capacity, all_random, out_scores, out_ids);
+}
+
+/* fp32 logits -> fp32 scores (SCORE_TYPE 2) */
+EXPORT int oracle_candidates_f32(const float* logits, int64_t rows, int64_t width, int64_t stride,
+                                 const float* temperatures, int64_t owned_rows, int count,
+                                 int capacity, int all_random, float* out_scores, int64_t* out_ids) {
+    return candidates_kind(logits, 2, rows, width, stride, temperatures, owned_rows, count, capacity,
+                           all_random, out_scores, out_ids);
 }
 
 EXPORT int oracle_candidates(const uint16_t* logits, int64_t rows, int64_t width, int64_t stride,

@@ -15,7 +15,7 @@ decode_cubic              reference.py:98-121                               clos
 decode_f16                quantization.py:181-182 with FP16 activations     numpy fp32->fp16 cast equals torch's on every decoded value
 linear_bf16               ops/eager/linear.py:43-56 + quantization.py:181  FP64 anchor + enclosure bound
 check_linear_enclosure    guardrail/quantization.py:176-320 (bf16, fp16)    closed form; rejects a +0.25 (bf16) / one-ulp-times-8 (fp16) corruption
-candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows (bf16 and fp16 scores)
+candidates                ops/cuda/sampling/local_candidates.{py,cu}        brute force argsort on tiny rows (bf16, fp16 and fp32 scores)
 verify_k1                 ops/cuda/sampling/speculative.py:46-219           reference KATs :73-131, :230-309; frozen-draw sweep :133-228; double-precision _oracle
 root_sample               ops/cuda/sampling/topk_topp.py:22-121             reference oracle KATs tests/ops/test_cuda_topk_topp_sampling.py:65-91 and CUDA-test expectations :127-201; float64 brute force with explicit uniforms
 moe_route                 ops/cuda/moe/fused.py:44-100                      stable argsort + float64 softmax (ids exact, weights within one bf16 step); reference softmax-midpoint KAT tests/unit/test_cuda_moe.py:276-332
@@ -279,6 +279,27 @@ def candidates(logits_bits: np.ndarray, temperatures: np.ndarray, count: int, ca
                                        ctypes.c_int(count), ctypes.c_int(capacity),
                                        ctypes.c_int(int(all_random)), ctypes.c_int(int(fp16)),
                                        _p(scores), _p(ids))
+    if rc:
+        raise ValueError("invalid candidate count")
+    ids[ids >= 0] += vocab_start
+    return scores, ids
+
+
+def candidates_f32(logits: np.ndarray, temperatures: np.ndarray, count: int, capacity: int | None = None,
+                   owned_rows: int | None = None, all_random: bool = False, vocab_start: int = 0):
+    """[M, V] float32 logits (SCORE_TYPE 2, local_candidates.py:41) -> ([M, capacity] float32
+    scores, [M, capacity] int64 ids); the rules of `candidates`, compared as float32 values."""
+    logits = _c(logits, np.float32)
+    rows, width = logits.shape
+    capacity = count if capacity is None else capacity
+    owned_rows = rows if owned_rows is None else owned_rows
+    temps = _c(temperatures, np.float32)
+    scores = np.empty((rows, capacity), np.float32)
+    ids = np.empty((rows, capacity), np.int64)
+    rc = lib().oracle_candidates_f32(_p(logits), ctypes.c_int64(rows), ctypes.c_int64(width),
+                                     ctypes.c_int64(width), _p(temps), ctypes.c_int64(owned_rows),
+                                     ctypes.c_int(count), ctypes.c_int(capacity),
+                                     ctypes.c_int(int(all_random)), _p(scores), _p(ids))
     if rc:
         raise ValueError("invalid candidate count")
     ids[ids >= 0] += vocab_start

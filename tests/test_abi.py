@@ -38,14 +38,21 @@ def test_host_planning_entry_points():
     assert lib.cubic_gemm_workspace_bytes(1, 4096, 12288, 4) < lib.cubic_gemm_workspace_bytes(64, 4096, 12288, 4)
     assert lib.cubic_accept_workspace_bytes(32, 1, 151936) > 0
     assert lib.cubic_accept_workspace_bytes(32, 9, 151936) == -1      # depth above 8
-    assert lib.cubic_candidates_workspace_bytes(64, 10**7) == -1      # vocabulary too wide
+    # one size for every logits dtype: the fp32 plan ([rows, 4096-column tiles, 20] u64 keys
+    # + flags) also covers vocabularies too wide for the 16-bit plan
+    assert lib.cubic_candidates_workspace_bytes(64, 151936) >= 64 * 38 * (20 * 8 + 4)
+    assert lib.cubic_candidates_workspace_bytes(64, 10**7) >= 64 * 2442 * (20 * 8 + 4)
 
 
 def test_invalid_arguments_fail_before_any_launch():
     with pytest.raises(ValueError, match="count"):
         _native.call("cubic_candidates", 16, 0, 100, 2, 100, 0, 16, 2, None, None, 21, 21, 0, 16, 16, 16, 1 << 20, None)
     with pytest.raises(ValueError, match="dtype"):
-        _native.call("cubic_candidates", 16, 2, 100, 2, 100, 0, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 20, None)
+        _native.call("cubic_candidates", 16, 3, 100, 2, 100, 0, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 20, None)
+    with pytest.raises(ValueError, match="too large"):   # 16-bit plan: at most 24 tiles of 32768
+        _native.call("cubic_candidates", 16, 0, 10**7, 2, 10**7, 0, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 30, None)
+    with pytest.raises(ValueError, match="workspace"):   # fp32 plan, workspace too small
+        _native.call("cubic_candidates", 16, 2, 10**7, 2, 10**7, 0, 16, 2, None, None, 20, 20, 0, 16, 16, 16, 1 << 10, None)
     with pytest.raises(ValueError, match="tp"):
         _native.call("cubic_verify_candidates", *([16] * 13), 0, 9, 4, 8, 20, 4, 16, None)
     with pytest.raises(ValueError, match="group_in"):

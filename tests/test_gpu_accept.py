@@ -127,6 +127,107 @@ def test_fp16_candidates_match_oracle(oracle, rows, width):
         assert (ids[2, :count] == -2).all()
 
 
+def _f32_case(rows, width, seed):
+    g = torch.Generator().manual_seed(seed)
+    logits = (torch.randn((rows, width), generator=g) * 3).numpy().astype(np.float32)
+    logits[0, 5] = logits[0, width - 1] = 64.0            # tie for the maximum across tiles
+    logits[0, 17], logits[0, 18] = np.float32(-0.0), np.float32(0.0)
+    if rows > 1:
+        logits[1, 7] = logits[1, width - 2] = 80.0        # greedy row: tie across tiles
+    if rows > 2:
+        logits[2, width // 3] = np.nan                    # non-finite row -> id -2
+    if rows > 4:
+        logits[4] = -np.abs(logits[4]) - 1.0             # greedy row: all negative but -0/+0
+        logits[4, width // 2], logits[4, width - 5] = np.float32(-0.0), np.float32(0.0)
+    if rows > 6:
+        logits[6, width - 1] = -np.inf                    # non-finite in the last tile
+    if rows > 7:
+        logits[7, :] = np.float32(1.5)                    # all equal: lowest ids
+    temps = np.array([(0.0 if r % 3 == 1 else 0.7) for r in range(rows)], np.float32)
+    return logits, temps
+
+
+@pytest.mark.parametrize("rows,width,pad", [(3, 300, 0), (5, 4097, 0), (8, 8192, 3), (64, 151936, 0),
+                                            (2, 400003, 1), (9, 20, 0)])
+def test_f32_candidates_match_oracle(oracle, rows, width, pad):
+    """fp32 logits (local_candidates.py:41, SCORE_TYPE 2): fp32 scores published bit
+    for bit, fp32 NaN padding, -2 for non-finite rows, ties by ascending id; an odd
+    row stride (pad) takes the one-column-per-lane loads."""
+    print(f"f32 candidates rows={rows} width={width} pad={pad}", flush=True)
+    logits, temps = _f32_case(rows, width, rows * 13 + width)
+    count, capacity = min(20, width), 24
+    owned = max(1, rows - 1)
+    dev_full = torch.zeros((rows, width + pad), dtype=torch.float32, device=DEV)
+    dev_full[:, :width] = torch.from_numpy(logits).to(DEV)
+    scores = torch.empty((rows, capacity), dtype=torch.float32, device=DEV)
+    ids = torch.empty((rows, capacity), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    plan = sampling.LocalCandidatePlan(local_logits=dev_full[:, :width], workspace=ws, active_rows=rows,
+                                       visible_width=width, local_count=count, owned_rows=owned)
+    want_s, want_i = oracle.candidates_f32(logits, temps, count, capacity, owned_rows=owned)
+    for _ in range(2):
+        scores.fill_(1.0)
+        ids.fill_(7)
+        plan.launch(temperatures=torch.from_numpy(temps).to(DEV))
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), want_i)
+        assert np.array_equal(scores.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    if owned > 2:
+        assert (ids[2, :count] == -2).all()
+
+
+@pytest.mark.parametrize("count,capacity,all_random", [(1, 1, False), (7, 64, False), (20, 64, True)])
+def test_f32_candidates_counts_offset_all_random(oracle, count, capacity, all_random):
+    rows, width, start = 9, 9000, 1000
+    logits, temps = _f32_case(rows, width, count * 31 + capacity)
+    scores = torch.empty((rows, capacity), dtype=torch.float32, device=DEV)
+    ids = torch.empty((rows, capacity), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    plan = sampling.LocalCandidatePlan(local_logits=torch.from_numpy(logits).to(DEV), workspace=ws,
+                                       active_rows=rows, visible_width=width, local_count=count,
+                                       vocab_start=start, all_random_rows=all_random)
+    plan.launch(temperatures=torch.from_numpy(temps).to(DEV))
+    torch.cuda.synchronize()
+    want_s, want_i = oracle.candidates_f32(logits, temps, count, capacity, all_random=all_random,
+                                           vocab_start=start)
+    assert np.array_equal(ids.cpu().numpy(), want_i)
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+
+
+def test_f32_candidates_device_metadata_in_graph(oracle):
+    """metadata[0] and row_activity read at replay (local_candidates.py:55-70), fp32."""
+    rows, width, count = 8, 20000, 20
+    logits, temps = _f32_case(rows, width, 99)
+    scores = torch.empty((rows, count), dtype=torch.float32, device=DEV)
+    ids = torch.empty((rows, count), dtype=torch.int64, device=DEV)
+    ws = sampling.ShardedSamplingWorkspace(scores, ids, scores, ids)
+    meta = torch.tensor([rows], dtype=torch.int32, device=DEV)
+    activity = torch.ones(rows, dtype=torch.bool, device=DEV)
+    plan = sampling.LocalCandidatePlan(local_logits=torch.from_numpy(logits).to(DEV), workspace=ws,
+                                       active_rows=rows, visible_width=width, local_count=count,
+                                       metadata=meta, row_activity=activity)
+    full_s, full_i = oracle.candidates_f32(logits, temps, count, count)
+    t_dev = torch.from_numpy(temps).to(DEV)
+    plan.launch(temperatures=t_dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.launch(temperatures=t_dev)
+    for n, act in ((rows, [1] * rows), (5, [1, 0, 1, 1, 0, 1, 1, 1]), (0, [1] * rows)):
+        meta[0] = n
+        activity.copy_(torch.tensor(act, dtype=torch.bool))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_s, got_i = scores.cpu().numpy().view(np.uint32), ids.cpu().numpy()
+        for r in range(rows):
+            if r < n and act[r]:
+                assert np.array_equal(got_i[r], full_i[r]), (n, r)
+                assert np.array_equal(got_s[r], full_s[r].view(np.uint32)), (n, r)
+            else:
+                assert (got_i[r] == -1).all() and (got_s[r] == 0x7FC00000).all(), (n, r)
+    graph.reset()
+
+
 def test_candidates_all_equal_row_takes_lowest_ids(oracle):
     rows, width = 2, 40000
     bits = np.full((rows, width), np.uint16(0x3F80), np.uint16)  # all 1.0

@@ -124,6 +124,47 @@ def test_fp16_candidates_match_brute_force_sort(oracle):
     assert (i2 == ids[:4]).all()
 
 
+def test_f32_candidates_match_brute_force_sort(oracle):
+    """fp32 logits (local_candidates.py:41, SCORE_TYPE 2): order by float32 value
+    with ascending ids on ties (-0 == +0), scores published bit for bit, fp32 NaN
+    padding, -2 for rows with a non-finite logit; all_random greedy rows pad."""
+    rng = np.random.default_rng(13)
+    rows, width, count = 6, 300, 20
+    logits = (np.round(rng.standard_normal((rows, width)) * 4) / 4).astype(np.float32)
+    logits[0, 40] = logits[0, 260] = 9.0                    # tie for the maximum
+    logits[2] = -np.abs(logits[2]) - 1.0
+    logits[2, 17], logits[2, 9] = np.float32(-0.0), np.float32(0.0)  # -0 ties with +0
+    logits[3, 5] = np.float32(1.4e-45)                         # smallest subnormal
+    logits[3, 6] = np.float32(np.nextafter(np.float32(0.25), np.float32(1)))  # one ulp above a tie
+    logits[5, 123] = -np.inf
+    temps = np.array([0.7, 0.0, 0.0, 1.0, 0.5, 1.0], np.float32)
+    scores, ids = oracle.candidates_f32(logits, temps, count, capacity=24)
+    bits = logits.view(np.uint32)
+    nan_bits = np.uint32(0x7FC00000)
+    for r in range(rows):
+        got = scores[r].view(np.uint32)
+        if r == 5:
+            assert (ids[r, :count] == -2).all() and (ids[r, count:] == -1).all()
+            assert (got == nan_bits).all()
+            continue
+        order = sorted(range(width), key=lambda j: (-float(logits[r, j]), j))
+        if temps[r] == 0:
+            assert ids[r, 0] == order[0] and got[0] == bits[r, order[0]]
+            assert (ids[r, 1:] == -1).all() and (got[1:] == nan_bits).all()
+        else:
+            assert ids[r, :count].tolist() == order[:count]
+            assert got[:count].tolist() == bits[r, order[:count]].tolist()
+            assert (ids[r, count:] == -1).all()
+    assert ids[0, 0] == 40 and ids[2, 0] == 9 and scores[2, 0].view(np.uint32) == 0  # +0 at id 9 first
+    # all_random: greedy rows publish padding; owned_rows pads the rest
+    s2, i2 = oracle.candidates_f32(logits, temps, count, capacity=24, all_random=True, owned_rows=4)
+    assert (i2[1] == -1).all() and (i2[2] == -1).all() and (i2[4:] == -1).all()
+    assert (i2[0] == ids[0]).all() and (i2[3] == ids[3]).all()
+    # the bf16 restatement agrees where the values are exact in bf16
+    b, bi = oracle.candidates(bf16(logits[:1]), temps[:1], count, capacity=24)
+    assert (bi == ids[:1]).all()
+
+
 # --------------------------------------------------------------------------- #
 # verify_k1: reference known answers
 # --------------------------------------------------------------------------- #
