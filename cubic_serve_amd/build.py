@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -45,6 +46,24 @@ def flags() -> list[str]:
     ]
 
 
+def resource_usage(remarks: str) -> dict[str, dict[str, int]]:
+    """Per-kernel counters from clang's kernel-resource-usage remarks."""
+    usage: dict[str, dict[str, int]] = {}
+    name = None
+    for line in remarks.splitlines():
+        if "remark:" not in line:
+            continue
+        text = line.split("remark:", 1)[1].split("[-Rpass", 1)[0].strip()
+        if text.startswith("Function Name:"):
+            name = text.split(":", 1)[1].strip()
+            usage[name] = {}
+        elif name and ":" in text:
+            key, val = (t.strip() for t in text.rsplit(":", 1))
+            if val.lstrip("-").isdigit():
+                usage[name][key] = int(val)
+    return usage
+
+
 def build(verbose: bool = False, jobs: int = 3) -> Path:
     """Compile every HIP source (in parallel) and link the shared library."""
     LIB_DIR.mkdir(exist_ok=True)
@@ -56,22 +75,45 @@ def build(verbose: bool = False, jobs: int = 3) -> Path:
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         objects.append(obj)
-        cmd = [cc, *flags(), *FILE_FLAGS.get(src, ()), "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *flags(), *FILE_FLAGS.get(src, ()), "-Rpass-analysis=kernel-resource-usage",
+               "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
-        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
-        while sum(p.poll() is None for _, p in procs) >= jobs:
-            procs[[p.poll() is None for _, p in procs].index(True)][1].wait()
+        # output to a file, not a pipe: the resource remarks run to megabytes,
+        # and a child blocked on a full pipe never exits
+        log = tempfile.TemporaryFile()
+        procs.append((src, subprocess.Popen(cmd, stdout=log, stderr=subprocess.STDOUT), log))
+        while sum(p.poll() is None for _, p, _ in procs) >= jobs:
+            procs[[p.poll() is None for _, p, _ in procs].index(True)][1].wait()
     failed = []
-    for src, p in procs:
-        out = p.communicate()[0].decode(errors="replace")
-        lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+    usage: dict[str, dict[str, int]] = {}
+    for src, p, log in procs:
+        p.wait()
+        log.seek(0)
+        out = log.read().decode(errors="replace")
+        log.close()
+        usage.update(resource_usage(out))
+        lines = [l for l in out.splitlines()
+                 if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l and "remark" not in l]
         if p.returncode != 0:
             failed.append((src, "\n".join(lines)))
-        elif verbose and lines:
+        elif verbose and any(l.strip() for l in lines):
             print("\n".join(lines))
     if failed:
         raise RuntimeError("HIP build failed:\n" + "\n\n".join(f"[{s}]\n{o}" for s, o in failed))
+    # No kernel may use scratch memory: a small array or struct indexed with
+    # a register, or an argument block copied for such an access, costs every
+    # launch (the large-M GEMM lost 20% to a 312-byte copy of its arguments).
+    # SGPR spills go to VGPR lanes and are not scratch.
+    with open(LIB_DIR / "resources.txt", "w") as f:
+        for name in sorted(usage):
+            u = usage[name]
+            f.write(f"{name} vgprs={u.get('VGPRs', -1)} sgprs={u.get('TotalSGPRs', -1)} "
+                    f"scratch={u.get('ScratchSize [bytes/lane]', -1)} occupancy={u.get('Occupancy [waves/SIMD]', -1)} "
+                    f"lds={u.get('LDS Size [bytes/block]', -1)}\n")
+    private = [n for n, u in usage.items() if u.get("ScratchSize [bytes/lane]", 0)]
+    if private:
+        raise RuntimeError("kernels using scratch memory:\n" + "\n".join(private[:20]))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)

@@ -236,6 +236,26 @@ __host__ __device__ constexpr int tile_cols() { return WV * J * 16; }
 template <int J, int WV = kGemmWaves>
 __host__ __device__ constexpr int tile_pitch() { return tile_cols<J, WV>() + 8; }
 
+// Output row m of a member, and a member's row stride, by constant indices
+// into the argument arrays: indexing them with a register makes the compiler
+// copy the whole argument block to private memory (scratch) in the
+// register-heavy kernels.
+__device__ __forceinline__ int64_t member_ldy(const GemmArgs& a, int member) {
+    int64_t ld = a.ldys[0];
+#pragma unroll
+    for (int i = 1; i < kMaxGemmMembers; ++i)
+        if (member == i) ld = a.ldys[i];
+    return ld;
+}
+
+__device__ __forceinline__ uint16_t* member_row(const GemmArgs& a, int member, int64_t m) {
+    uint16_t* y = a.ys[0];
+#pragma unroll
+    for (int i = 1; i < kMaxGemmMembers; ++i)
+        if (member == i) y = a.ys[i];
+    return y + m * member_ldy(a, member);
+}
+
 template <int J, int MT, int WV = kGemmWaves>
 __device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* tile, int m0) {
     constexpr int C = tile_cols<J, WV>(), P = tile_pitch<J, WV>();
@@ -249,8 +269,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* ti
     const int member0 = n_base / a.n_member;
     const int nl0 = n_base - member0 * a.n_member;
     if (n_base + C <= a.n && nl0 + C <= a.n_member) {
-        uint16_t* y0 = a.ys[member0] + nl0;
-        const int64_t ldy = a.ldys[member0];
+        uint16_t* y0 = member_row(a, member0, 0) + nl0;
+        const int64_t ldy = member_ldy(a, member0);
         if (((reinterpret_cast<uintptr_t>(y0) | (uintptr_t)ldy * 2) & 15) == 0) {
 #pragma unroll
             for (int i = 0; i < (kChunks + kThr - 1) / kThr; ++i) {
@@ -276,15 +296,18 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const uint16_t* ti
         const uint4 v = *reinterpret_cast<const uint4*>(&tile[row * P + seg * 8]);
         const int member = n / a.n_member;
         const int nl = n - member * a.n_member;
-        uint16_t* y = a.ys[member] + (int64_t)m * a.ldys[member] + nl;
+        uint16_t* y = member_row(a, member, m) + nl;
         if (nl + 8 <= a.n_member && n + 8 <= a.n && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
             *reinterpret_cast<uint4*>(y) = v;
         } else {
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            for (int e = 0; e < 8 && n + e < a.n; ++e) {
-                const int ne = n + e, me = ne / a.n_member;
-                a.ys[me][(int64_t)m * a.ldys[me] + (ne - me * a.n_member)] =
-                    (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int ne = n + e;
+                if (ne < a.n) {
+                    const int me = ne / a.n_member;
+                    const uint32_t word = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+                    member_row(a, me, m)[ne - me * a.n_member] = (uint16_t)(word >> (16 * (e & 1)));
+                }
             }
         }
     }
