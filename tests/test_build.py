@@ -6,6 +6,8 @@ from __future__ import annotations
 
 from pathlib import Path
 
+import pytest
+
 from cubic_serve_amd import build
 
 REMARKS = """\
@@ -38,7 +40,7 @@ def test_built_library_has_no_scratch_kernels():
     kernel and none uses scratch (the build refuses otherwise)."""
     summary = Path(build.LIB_DIR) / "resources.txt"
     if not summary.exists():
-        return
+        pytest.skip("library not built in this tree")
     lines = summary.read_text().splitlines()
     assert len(lines) > 100
     assert all(" scratch=0 " in ln for ln in lines), [ln for ln in lines if " scratch=0 " not in ln][:3]
