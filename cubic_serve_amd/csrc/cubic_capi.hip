@@ -91,18 +91,32 @@ bool small_rows(int64_t m, int bits, int group_in, int64_t k) {
 
 // K partition of one member: split in powers of two (at most 8) until a
 // partition holds at most 16 k-blocks -- 32 when the unsplit member already
-// gives >= 384 workgroups of one tile per wave -- and about 256 workgroups of
-// one tile per wave are in flight; a member wide enough to fill the GPU with
-// two tiles per wave keeps K whole.  (The 32-block cap: Llama-3-70B gate/up
-// members, 28672 x 8192, split 2 instead of 4: grouped launch 607 -> 521 us
-// at M = 512, 61 -> 57 at M = 8, equal at M = 64, same box.)
-void plan_k(int64_t n_member, int64_t k, int* split_out, int* bps_out) {
+// gives >= 160 workgroups of one tile per wave, 64 for a K of 128 k-blocks or
+// more -- and about 256 workgroups of one tile per wave are in flight; a
+// member wide enough to fill the GPU with two tiles per wave keeps K whole.
+// The plan is a function of one member's (n, k) alone, so a row's result does
+// not depend on M.  Measured per launch, same box, W4, M = 8 / 64 / 512 (us):
+//   Llama-3-70B gate/up members, 28672 x 8192: split 2 instead of 4, grouped
+//     launch 61 -> 57, equal, 607 -> 521;
+//   qkv 10240 x 8192: split 2 instead of 4, 19.6 -> 19.4, 33.3 -> 31.1,
+//     123.9 -> 117.0;
+//   down 8192 x 28672: split 4 instead of 8, 34.3 -> 31.3, 53.9 -> 56.8,
+//     284 -> 255;
+//   o 8192 x 8192 stays at 4 (split 2: 13.7 -> 18.3 and 21.6 -> 28.3 at
+//     M = 8 and 64, though 99 -> 81 at M = 512).
+// Above 4 bits (per-weight curve or LDS-table decode, about twice the work
+// per weight) the 160-block and deep-K caps lose: qkv and down at 6 and 8 bits
+// take 16-22 us longer at M = 8 and 64 with the halved split, so there the
+// cap is 32 only from 384 workgroups.  Bits are a property of the weight, so
+// the plan still does not depend on M.
+void plan_k(int64_t n_member, int64_t k, int bits, int* split_out, int* bps_out) {
     const int64_t tiles = ceil_div(n_member, 16);
     const int k_blocks = (int)ceil_div(k, kKBlock);
     int split = 1;
     if (ceil_div(tiles, 2 * cubic::kGemmWaves) < 256) {
         const int64_t out_blocks = ceil_div(tiles, cubic::kGemmWaves);
-        const int kb_cap = out_blocks >= 384 ? 32 : 16;
+        const int kb_cap = bits > 4 ? (out_blocks >= 384 ? 32 : 16)
+                                    : (k_blocks >= 128 ? 64 : out_blocks >= 160 ? 32 : 16);
         while (split < 8 && (ceil_div(k_blocks, split) > kb_cap || out_blocks * split < 256)) split *= 2;
         if (split > k_blocks / 2) split = k_blocks / 2 > 0 ? k_blocks / 2 : 1;
     }
@@ -129,7 +143,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n_member, int members, int64_t k, int bits
     p.panel = 0;
     p.panel_stages = 2;
     p.panel_waves = cubic::kGemmWaves;
-    plan_k(n_member, k, &p.split, &p.blocks_per_split);
+    plan_k(n_member, k, bits, &p.split, &p.blocks_per_split);
 #ifdef CUBIC_EXPERIMENTS
     if (g_exp_split > 0) {
         p.split = g_exp_split;
