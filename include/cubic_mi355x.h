@@ -89,7 +89,7 @@ CUBIC_API int cubic_prepare_weight(int fmt, const void* packed, const void* m0, 
  * and the small-row kernel of quantization/common/small_rows.cu:94-241.
  *
  * K plan: the K partition of every output column is a function of its
- * member's (n, k) only -- never of m, nor of how many members share a launch
+ * member's (n, k) and bits only -- never of m, nor of how many members share a launch
  * (quantization/extensions/cubic/marlin.py:347-360, common/marlin/cost.py:
  * 59-79) -- so a row's result is bitwise the same for every m of one
  * arithmetic regime and grouped members equal separate launches bit for bit.
