@@ -534,7 +534,9 @@ def measure_cfg1(dev) -> dict:
 
     step_ms = time_graph(capture(lambda: [one_step() for _ in range(len(binds))]), 10, 2) / len(binds)
     merged = plan.merged.cpu().tolist()
+    floor_ms = stream_floor_ms(gemm_bytes(2, n, k))
     return {"lm_head_us": round(lm_ms * 1e3, 2), "lm_head_gbs": round(gemm_bytes(2, n, k) / lm_ms / 1e6, 1),
+            "lm_head_floor_us": round(floor_ms * 1e3, 2), "lm_head_floor_frac": round(floor_ms / lm_ms, 4),
             "accept_us": round(acc_ms * 1e3, 2), "verify_step_us": round(step_ms * 1e3, 2),
             "accepted": merged[0][0]}
 
