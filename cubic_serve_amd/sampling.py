@@ -256,7 +256,16 @@ class LocalCandidatePlan:
     def __init__(self, *, local_logits: Tensor, workspace: ShardedSamplingWorkspace,
                  active_rows: int, visible_width: int, local_count: int, vocab_start: int = 0,
                  owned_rows: int | None = None, all_random_rows: bool = False,
-                 row_activity: Tensor | None = None, metadata: Tensor | None = None) -> None:
+                 row_activity: Tensor | None = None, metadata: Tensor | None = None,
+                 token_mask: Tensor | None = None, masked_logits: Tensor | None = None,
+                 consume_logits: bool = False) -> None:
+        # the reference's grammar variant (local_candidates.py:79-110, the
+        # HAS_GRAMMAR kernels of local_candidates.cu) is reached from its
+        # greedy sampler only; cubic_serve_amd.greedy applies the mask inside
+        # the greedy launch.  The candidate plan itself does not admit it.
+        if token_mask is not None or masked_logits is not None or consume_logits:
+            raise ValueError("grammar-masked candidate preparation is not admitted by this build "
+                             "(use cubic_serve_amd.greedy for masked greedy sampling)")
         if (local_logits.dtype not in _CANDIDATE_DTYPES or local_logits.ndim != 2
                 or local_logits.stride(1) != 1
                 or not 0 < active_rows <= local_logits.shape[0]

@@ -149,3 +149,21 @@ def test_greedy_sampler_arguments():
     with pytest.raises(ValueError, match="exceeds the vocabulary"):
         _native.call("cubic_greedy_sample", 16, 0, 100, 4, 100, 16, None, 0, 20, 16, 16, 16, 16, 16, 99,
                      16, 16, 16, 16, 16, 16, ws, None)
+
+
+def test_candidate_plan_refuses_grammar_masks():
+    """The grammar variant of LocalCandidatePlan (token_mask, masked_logits,
+    consume_logits: local_candidates.py:79-110) is refused at bind, before any
+    device work, with a message naming the masked greedy path."""
+    import torch
+    from cubic_serve_amd import sampling
+    logits = torch.zeros((2, 64), dtype=torch.bfloat16)
+    s = torch.empty((2, 20), dtype=torch.bfloat16)
+    i = torch.empty((2, 20), dtype=torch.int64)
+    ws = sampling.ShardedSamplingWorkspace(s, i, s, i)
+    with pytest.raises(ValueError, match="grammar"):
+        sampling.LocalCandidatePlan(local_logits=logits, workspace=ws, active_rows=2, visible_width=64,
+                                    local_count=20, token_mask=torch.zeros((2, 2), dtype=torch.int32))
+    with pytest.raises(ValueError, match="grammar"):
+        sampling.LocalCandidatePlan(local_logits=logits, workspace=ws, active_rows=2, visible_width=64,
+                                    local_count=20, consume_logits=True)
