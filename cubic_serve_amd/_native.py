@@ -16,7 +16,7 @@ P = ctypes.c_void_p
 I32 = ctypes.c_int
 I64 = ctypes.c_int64
 
-ABI_VERSION = 5  # cubic_abi_version() of the library these signatures describe
+ABI_VERSION = 6  # cubic_abi_version() of the library these signatures describe
 
 # name -> (restype, argtypes); mirrors include/cubic_mi355x.h
 SIGNATURES: dict[str, tuple] = {
@@ -48,11 +48,11 @@ SIGNATURES: dict[str, tuple] = {
     "cubic_root_sample": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P, P]),
     "cubic_merge_prefix": (I32, [P, I32, I32, P, I32, P, P]),
     "cubic_greedy_workspace_bytes": (I64, [I32, I32]),
-    "cubic_greedy_candidates": (I32, [P, I32, I64, I32, I32, I64, P, P, I64, I32, P, P, P, I64, P]),
+    "cubic_greedy_candidates": (I32, [P, I32, I64, I32, I32, I64, P, P, I64, P, I64, I32, P, P, P, I64, P]),
     "cubic_greedy_root": (I32, [P, I32, P, P, P, P, P, P, P, I32, I32, I32, I64, P, P, P]),
     "cubic_sampling_final_guard": (I32, [P, P, P, P, P, P, P, P, I32, I32, I64, P, P]),
-    "cubic_greedy_sample": (I32, [P, I32, I64, I32, I32, P, P, I64, I32, P, P, P, P, P, I64, P, P, P,
-                                  P, P, P, I64, P]),
+    "cubic_greedy_sample": (I32, [P, I32, I64, I32, I32, P, P, I64, P, I64, I32, P, P, P, P, P, I64, P,
+                                  P, P, P, P, P, I64, P]),
     "cubic_accept_workspace_bytes": (I64, [I32, I32, I32]),
     "cubic_accept": (I32, [P, I64, I32, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P, P, P, P, P,
                            P, P, P, P, I64, P]),

@@ -408,7 +408,7 @@ int accept_common(const void* logits, int64_t row_stride, int width, int c, int 
 
 extern "C" {
 
-int cubic_abi_version(void) { return 5; }
+int cubic_abi_version(void) { return 6; }
 
 const char* cubic_last_error(void) { return g_error.c_str(); }
 
@@ -898,8 +898,9 @@ bool greedy_params(const float* temperatures, const float* top_ps, const int64_t
 
 int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int rows, int width,
                 int64_t vocab_start, const int32_t* metadata, const uint32_t* token_mask,
-                int64_t mask_words, int candidates, void* scores, int64_t* ids, void* workspace,
-                int64_t workspace_bytes, cubic::GreedyArgs& a, const char* who) {
+                int64_t mask_words, void* masked_logits, int64_t masked_stride, int candidates,
+                void* scores, int64_t* ids, void* workspace, int64_t workspace_bytes,
+                cubic::GreedyArgs& a, const char* who) {
     if (!logits || !metadata || !scores || !ids || !workspace) return fail(CUBIC_EINVAL, "%s: null operand", who);
     if (rows < 1 || rows > 65535 || width < 0 || width > kGreedyMaxWidth || row_stride < width)
         return fail(CUBIC_EINVAL, "%s: invalid logits geometry", who);
@@ -907,6 +908,11 @@ int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int row
     if (candidates < 1 || candidates > 64) return fail(CUBIC_EINVAL, "%s: need 1 <= candidates <= 64", who);
     if (token_mask && (mask_words < 1 || vocab_start + width > mask_words * 32))
         return fail(CUBIC_EINVAL, "%s: grammar mask rows do not cover the visible vocabulary", who);
+    if (masked_logits && !token_mask)
+        return fail(CUBIC_EINVAL, "%s: masked logits need a grammar mask", who);
+    const bool inplace = masked_logits == logits;
+    if (masked_logits && (masked_stride < width || (inplace && masked_stride != row_stride)))
+        return fail(CUBIC_EINVAL, "%s: masked logits geometry (in place: the logits' own row stride)", who);
     const int64_t need = greedy_workspace(rows, width);
     if (workspace_bytes < need)
         return fail(CUBIC_EWORKSPACE, "%s: workspace %lld < %lld", who, (long long)workspace_bytes, (long long)need);
@@ -920,6 +926,9 @@ int greedy_pass(const void* logits, int logits_fp16, int64_t row_stride, int row
     a.metadata = metadata;
     a.token_mask = token_mask;
     a.mask_words = mask_words;
+    a.masked = (uint16_t*)masked_logits;
+    a.masked_stride = masked_stride;
+    a.masked_inplace = masked_logits && inplace;
     a.candidates = candidates;
     a.scores = (uint16_t*)scores;
     a.ids = ids;
@@ -950,13 +959,13 @@ int64_t cubic_greedy_workspace_bytes(int rows, int width) {
 
 int cubic_greedy_candidates(const void* logits, int logits_fp16, int64_t row_stride, int rows,
                             int width, int64_t vocab_start, const int32_t* metadata,
-                            const uint32_t* token_mask, int64_t mask_words, int candidates,
-                            void* scores, int64_t* ids, void* workspace, int64_t workspace_bytes,
-                            void* stream) {
+                            const uint32_t* token_mask, int64_t mask_words, void* masked_logits,
+                            int64_t masked_stride, int candidates, void* scores, int64_t* ids,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
     cubic::GreedyArgs a = {};
     const int rc = greedy_pass(logits, logits_fp16, row_stride, rows, width, vocab_start, metadata,
-                               token_mask, mask_words, candidates, scores, ids, workspace,
-                               workspace_bytes, a, "cubic_greedy_candidates");
+                               token_mask, mask_words, masked_logits, masked_stride, candidates,
+                               scores, ids, workspace, workspace_bytes, a, "cubic_greedy_candidates");
     if (rc != CUBIC_OK) return rc;
     return hip_status(cubic::launch_greedy(a, (hipStream_t)stream), "cubic_greedy_candidates launch");
 }
@@ -1004,7 +1013,8 @@ int cubic_sampling_final_guard(const int64_t* tokens, const uint8_t* root_valid,
 
 int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride, int rows,
                         int width, const int32_t* metadata, const uint32_t* token_mask,
-                        int64_t mask_words, int k, const float* temperatures, const float* top_ps,
+                        int64_t mask_words, void* masked_logits, int64_t masked_stride, int k,
+                        const float* temperatures, const float* top_ps,
                         const int64_t* top_ks, const int64_t* seeds, const int64_t* ordinals,
                         int64_t vocab_size, void* scores, int64_t* ids, int64_t* tokens,
                         uint8_t* root_valid, uint8_t* final_valid, void* workspace,
@@ -1017,8 +1027,8 @@ int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride,
         return fail(CUBIC_EINVAL, "cubic_greedy_sample: visible width exceeds the vocabulary");
     if (rows > 65535) return fail(CUBIC_EINVAL, "cubic_greedy_sample: at most 65535 rows");
     const int rc = greedy_pass(logits, logits_fp16, row_stride, rows, width, 0, metadata, token_mask,
-                               mask_words, k, scores, ids, workspace, workspace_bytes, a,
-                               "cubic_greedy_sample");
+                               mask_words, masked_logits, masked_stride, k, scores, ids, workspace,
+                               workspace_bytes, a, "cubic_greedy_sample");
     if (rc != CUBIC_OK) return rc;
     a.tokens = tokens;
     a.root_valid = root_valid;

@@ -205,6 +205,12 @@ struct GreedyArgs {
     const int32_t* metadata;      // [2]: active rows, cancel flag
     const uint32_t* token_mask;   // [rows, mask_words] or null
     int64_t mask_words;
+    // grammar-masked logits out (token_mask only): [rows, masked_stride], the
+    // logits' type; rows < active get the admitted logits and -inf elsewhere,
+    // other rows -inf unless masked == logits (in place: left as they are)
+    uint16_t* masked;
+    int64_t masked_stride;
+    int masked_inplace;
     int candidates;               // published slots per row
     uint16_t* scores;             // [rows, candidates]
     int64_t* ids;

@@ -217,6 +217,9 @@ __global__ __launch_bounds__(NT) void greedy_kernel(GreedyArgs a) {
                             if constexpr (MASK) {
                                 const int64_t token = a.vocab_start + j + e;
                                 admitted = (mask_row[token >> 5] >> (token & 31)) & 1u;
+                                if (a.masked)
+                                    a.masked[(int64_t)row * a.masked_stride + j + e] =
+                                        admitted ? (uint16_t)u : (uint16_t)(HALF ? 0xFC00u : 0xFF80u);
                             }
                             if (admitted) acc[e] = max(acc[e], (order16(u) << 16) | c);
                         }
@@ -224,6 +227,12 @@ __global__ __launch_bounds__(NT) void greedy_kernel(GreedyArgs a) {
                 }
             }
         }
+    }
+    if (MASK && a.masked && !a.masked_inplace && row >= active) {
+        // rows past the active count: every visible column of the tile is -inf
+        const uint32_t end = min(begin + (uint32_t)a.tile_width, (uint32_t)a.width);
+        for (uint32_t j = begin + threadIdx.x; j < end; j += NT)
+            a.masked[(int64_t)row * a.masked_stride + j] = (uint16_t)(HALF ? 0xFC00u : 0xFF80u);
     }
     good &= max(mag_max & 0xFFFFu, mag_max >> 16) < (HALF ? 0x7C00u : 0x7F80u);
     uint64_t key = 0;

@@ -75,6 +75,30 @@ def _mask_words(token_mask: Tensor | None, rows: int, device: torch.device) -> i
     return token_mask.shape[1]
 
 
+def _masked_output(logits: Tensor, rows: int, width: int, token_mask: Tensor | None,
+                   masked_logits: Tensor | None, consume_logits: bool) -> tuple[Tensor | None, int]:
+    """The grammar-masked logits output and its row stride, checked as the
+    reference's candidate preparation checks it (local_candidates.py:88-110):
+    consuming the logits (masking them in place) needs the mask; an explicit
+    output is [rows, width] of the logits' dtype on their device, contiguous
+    and in storage of its own unless it is the logits themselves."""
+    if type(consume_logits) is not bool or consume_logits and token_mask is None:
+        raise TensorParallelSamplingError("logits consumption requires an explicit masked terminal consumer")
+    if consume_logits and masked_logits is None:
+        masked_logits = logits[:rows, :width]
+    if masked_logits is None:
+        return None, 0
+    if (token_mask is None or masked_logits.shape != (rows, width) or masked_logits.dtype != logits.dtype
+            or masked_logits.device != logits.device
+            or (not consume_logits and not masked_logits.is_contiguous())
+            or (consume_logits and (masked_logits.data_ptr() != logits.data_ptr()
+                                    or masked_logits.stride() != logits[:rows, :width].stride()))
+            or (not consume_logits and masked_logits.untyped_storage().data_ptr()
+                == logits.untyped_storage().data_ptr())):
+        raise TensorParallelSamplingError("masked logits differ from the grammar consumer ABI")
+    return masked_logits, masked_logits.stride(0)
+
+
 def greedy_workspace(rows: int, width: int, device: torch.device) -> Tensor:
     """Zero-filled workspace for the candidate pass (every launch returns its
     arrival counters to zero, so one fill serves every later launch)."""
@@ -86,9 +110,12 @@ def greedy_workspace(rows: int, width: int, device: torch.device) -> Tensor:
 
 def greedy_candidates(logits: Tensor, metadata: Tensor, scores: Tensor, token_ids: Tensor,
                       workspace: Tensor, *, width: int | None = None, vocab_start: int = 0,
-                      token_mask: Tensor | None = None) -> None:
+                      token_mask: Tensor | None = None, masked_logits: Tensor | None = None,
+                      consume_logits: bool = False) -> None:
     """Exact argmax candidates of ``logits[:metadata[0], :width]`` into slot 0
-    of ``scores``/``token_ids`` [rows, K] (greedy.cu:14-78)."""
+    of ``scores``/``token_ids`` [rows, K] (greedy.cu:14-78).  With a grammar
+    mask, ``masked_logits`` [rows, width] (or the logits themselves, when
+    ``consume_logits``) receives the masked logits (local_candidates.cu:37-53)."""
     if logits.dtype not in (torch.bfloat16, torch.float16) or logits.ndim != 2 or logits.stride(1) != 1:
         raise TensorParallelSamplingError("greedy logits must be bf16/fp16 [rows, V] with unit column stride")
     rows = logits.shape[0]
@@ -101,11 +128,13 @@ def greedy_candidates(logits: Tensor, metadata: Tensor, scores: Tensor, token_id
     _require(scores, (rows, k), logits.dtype, dev, "candidate scores")
     _require(token_ids, (rows, k), torch.int64, dev, "candidate ids")
     words = _mask_words(token_mask, rows, dev)
+    masked, masked_stride = _masked_output(logits, rows, width, token_mask, masked_logits, consume_logits)
     with torch.cuda.device(dev):
         _native.call("cubic_greedy_candidates", logits.data_ptr(), int(logits.dtype == torch.float16),
                      logits.stride(0), rows, width, vocab_start, metadata.data_ptr(),
-                     _native.ptr(token_mask), words, k, scores.data_ptr(), token_ids.data_ptr(),
-                     workspace.data_ptr(), workspace.numel(), _native.stream_of(dev))
+                     _native.ptr(token_mask), words, _native.ptr(masked), masked_stride, k,
+                     scores.data_ptr(), token_ids.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                     _native.stream_of(dev))
 
 
 def greedy_root(gathered_scores: Tensor, gathered_token_ids: Tensor,
@@ -162,7 +191,8 @@ class CapturedGreedySampler:
     def __init__(self, *, local_logits: Tensor, true_vocab_size: int, token_ids: Tensor,
                  parameters: ShardedSamplingParameters, workspace: ShardedSamplingWorkspace,
                  root_valid: Tensor, capture_stream: torch.cuda.Stream | None = None,
-                 token_mask: Tensor | None = None, graph_pool=None) -> None:
+                 token_mask: Tensor | None = None, masked_logits: Tensor | None = None,
+                 graph_pool=None, consume_logits: bool = False) -> None:
         dev = token_ids.device
         self.device = dev
         self.capacity = token_ids.numel()
@@ -185,6 +215,8 @@ class CapturedGreedySampler:
         self.logits, self.token_ids, self.root_valid = local_logits, token_ids, root_valid
         self.parameters, self.workspace, self.token_mask = parameters, workspace, token_mask
         self._mask_words = _mask_words(token_mask, self.capacity, dev)
+        self.masked_logits, self._masked_stride = _masked_output(
+            local_logits, self.capacity, self.width, token_mask, masked_logits, consume_logits)
         self.metadata = torch.zeros(2, dtype=torch.int32, device=dev)
         self._metadata_hosts = torch.empty((self.capacity + 1, 2, 2), dtype=torch.int32, pin_memory=True)
         self._metadata_hosts[:, :, 0] = torch.arange(self.capacity + 1)[:, None]
@@ -212,7 +244,8 @@ class CapturedGreedySampler:
             _native.call("cubic_greedy_sample", self.logits.data_ptr(),
                          int(self.logits.dtype == torch.float16), self.logits.stride(0),
                          self.capacity, self.width, self.metadata.data_ptr(),
-                         _native.ptr(self.token_mask), self._mask_words, p.max_top_k,
+                         _native.ptr(self.token_mask), self._mask_words,
+                         _native.ptr(self.masked_logits), self._masked_stride, p.max_top_k,
                          *_param_ptrs(p), self.vocab_size, w.local_scores.data_ptr(),
                          w.local_token_ids.data_ptr(), self.token_ids.data_ptr(),
                          self.root_valid.data_ptr(), self.final_valid.data_ptr(),

@@ -38,8 +38,9 @@ extern "C" {
 
 /* ABI revision, raised whenever an entry point's arguments change: 2 added
  * the GEMM dtype, 3 the candidate dtype, 4 the device live/owned counts of
- * cubic_accept(_noalloc) and cubic_candidates, 5 the candidate vocab_start.
- * This header describes revision 5. */
+ * cubic_accept(_noalloc) and cubic_candidates, 5 the candidate vocab_start,
+ * 6 the grammar-masked logits output of the greedy launches.
+ * This header describes revision 6. */
 CUBIC_API int cubic_abi_version(void);
 CUBIC_API const char* cubic_last_error(void);
 
@@ -210,6 +211,14 @@ CUBIC_API int cubic_root_sample(const void* scores, int scores_fp16, const int64
  *   logits       bf16 (logits_fp16 = 0) or fp16 [rows, row_stride]
  *   token_mask   int32 bit words [rows, mask_words] (bit t%32 of word t/32
  *                admits token t) or NULL; needs vocab_start + width <= 32 * mask_words
+ *   masked_logits  logits dtype [rows, masked_stride] or NULL (token_mask
+ *                required): the grammar-masked logits the reference's candidate
+ *                preparation writes for its terminal consumer
+ *                (local_candidates.cu:37-53): row r < active, column j < width
+ *                gets logits[r, j] if the mask admits token vocab_start + j, else
+ *                -inf; rows >= active get -inf.  masked_logits == logits with
+ *                masked_stride == row_stride masks in place (consume_logits) and
+ *                leaves rows >= active as they are.
  *   scores/ids   logits dtype / int64 [rows, candidates], 1 <= candidates <= 64
  *   1 <= rows <= 65535, 0 <= width <= 2^30
  *   workspace    cubic_greedy_workspace_bytes(rows, width) bytes, zero-filled
@@ -243,7 +252,8 @@ CUBIC_API int64_t cubic_greedy_workspace_bytes(int rows, int width);
 CUBIC_API int cubic_greedy_candidates(const void* logits, int logits_fp16, int64_t row_stride,
                                       int rows, int width, int64_t vocab_start,
                                       const int32_t* metadata, const uint32_t* token_mask,
-                                      int64_t mask_words, int candidates, void* scores,
+                                      int64_t mask_words, void* masked_logits,
+                                      int64_t masked_stride, int candidates, void* scores,
                                       int64_t* ids, void* workspace, int64_t workspace_bytes,
                                       void* stream);
 CUBIC_API int cubic_greedy_root(const void* scores, int scores_fp16, const int64_t* ids,
@@ -260,7 +270,8 @@ CUBIC_API int cubic_sampling_final_guard(const int64_t* tokens, const uint8_t* r
                                          void* stream);
 CUBIC_API int cubic_greedy_sample(const void* logits, int logits_fp16, int64_t row_stride, int rows,
                                   int width, const int32_t* metadata, const uint32_t* token_mask,
-                                  int64_t mask_words, int k, const float* temperatures,
+                                  int64_t mask_words, void* masked_logits, int64_t masked_stride,
+                                  int k, const float* temperatures,
                                   const float* top_ps, const int64_t* top_ks, const int64_t* seeds,
                                   const int64_t* ordinals, int64_t vocab_size, void* scores,
                                   int64_t* ids, int64_t* tokens, uint8_t* root_valid,

@@ -23,7 +23,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_native.SIGNATURES), "ctypes signatures drift from the header"
-    assert lib.cubic_abi_version() == 5
+    assert lib.cubic_abi_version() == 6
 
 
 def test_host_planning_entry_points():
@@ -135,11 +135,15 @@ def test_greedy_sampler_arguments():
     assert lib.cubic_greedy_workspace_bytes(0, 100) == -1
     ws = lib.cubic_greedy_workspace_bytes(4, 100)
     with pytest.raises(ValueError, match="candidates"):
-        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, 65, 16, 16, 16, ws, None)
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, None, 0, 65, 16, 16, 16, ws, None)
     with pytest.raises(ValueError, match="grammar mask"):
-        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, 16, 3, 20, 16, 16, 16, ws, None)
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, 16, 3, None, 0, 20, 16, 16, 16, ws, None)
+    with pytest.raises(ValueError, match="masked logits need a grammar mask"):
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, 32, 100, 20, 16, 16, 16, ws, None)
+    with pytest.raises(ValueError, match="masked logits geometry"):   # in place needs the logits' stride
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, 16, 4, 16, 128, 20, 16, 16, 16, ws, None)
     with pytest.raises(ValueError, match="workspace"):
-        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, 20, 16, 16, 16, ws - 1, None)
+        _native.call("cubic_greedy_candidates", 16, 0, 100, 4, 100, 0, 16, None, 0, None, 0, 20, 16, 16, 16, ws - 1, None)
     with pytest.raises(ValueError, match="TP<=8"):
         _native.call("cubic_greedy_root", 16, 0, 16, 16, 16, 16, 16, 16, 16, 9, 4, 20, 100, 16, 16, None)
     with pytest.raises(ValueError, match="vocabulary"):
@@ -147,7 +151,7 @@ def test_greedy_sampler_arguments():
     with pytest.raises(ValueError, match="null"):
         _native.call("cubic_sampling_final_guard", 16, None, 16, None, 16, 16, 16, 16, 4, 20, 100, 16, None)
     with pytest.raises(ValueError, match="exceeds the vocabulary"):
-        _native.call("cubic_greedy_sample", 16, 0, 100, 4, 100, 16, None, 0, 20, 16, 16, 16, 16, 16, 99,
+        _native.call("cubic_greedy_sample", 16, 0, 100, 4, 100, 16, None, 0, None, 0, 20, 16, 16, 16, 16, 16, 99,
                      16, 16, 16, 16, 16, 16, ws, None)
 
 

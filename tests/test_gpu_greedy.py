@@ -218,7 +218,7 @@ def test_fused_sample_equals_composition(oracle, dtype, rows, width):
             if fused:
                 from cubic_serve_amd import _native
                 _native.call("cubic_greedy_sample", logits.data_ptr(), int(dtype == torch.float16),
-                             logits.stride(0), rows, width, meta.data_ptr(), None, 0, 20,
+                             logits.stride(0), rows, width, meta.data_ptr(), None, 0, None, 0, 20,
                              *greedy._param_ptrs(p), width, ws.local_scores.data_ptr(),
                              ws.local_token_ids.data_ptr(), tokens.data_ptr(), rv.data_ptr(),
                              final.data_ptr(), scratch.data_ptr(), scratch.numel(),
@@ -289,3 +289,93 @@ def test_captured_sampler_reference_corpus(oracle, dtype):
         finally:
             plan.close()
     assert side.item() > 0
+
+
+def _expected_masked(logits_bits, mask, start, active, ninf):
+    """local_candidates.cu:37-53: row r < active keeps the admitted columns'
+    bits and -inf elsewhere; rows >= active are -inf."""
+    rows, width = logits_bits.shape
+    words = mask.cpu().numpy().view(np.uint32)
+    tok = start + np.arange(width)
+    admitted = ((words[:, tok >> 5] >> (tok & 31).astype(np.uint32)) & 1).astype(bool)
+    out = np.where(admitted, logits_bits, np.uint16(ninf))
+    out[active:] = np.uint16(ninf)
+    return out
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_masked_logits_output_and_consumption(oracle, dtype):
+    """The grammar-masked logits the reference's candidate preparation writes
+    (masked_logits, or the logits themselves with consume_logits): admitted
+    columns bit for bit, -inf elsewhere, rows past the active count -inf (left
+    as they are when consumed); the published candidates are unchanged."""
+    gen = torch.Generator().manual_seed(21)
+    rows, width, start, active = 6, 5000, 37, 4
+    ninf = 0xFC00 if dtype == torch.float16 else 0xFF80
+    words = (start + width + 31) // 32 + 1
+    logits = tie_logits(rows, width + 3, dtype, gen)[:, :width]          # strided rows
+    mask = torch.randint(-2**31, 2**31, (rows, words), generator=gen, dtype=torch.int64).to(torch.int32)
+    mask[2] = 0                                                           # a row the grammar empties
+    mask = mask.to(DEV)
+    k = 20
+    scores = torch.empty((rows, k), dtype=dtype, device=DEV)
+    ids = torch.empty((rows, k), dtype=torch.int64, device=DEV)
+    ws = greedy.greedy_workspace(rows, width, DEV)
+    want = _expected_masked(bits(logits), mask, start, active, ninf)
+    want_s, want_i = oracle.greedy_candidates(bits(logits), active, k, fp16=dtype == torch.float16,
+                                              vocab_start=start, token_mask=mask.cpu().numpy().view(np.uint32))
+    # explicit output
+    out = torch.full((rows, width), 1.0, dtype=dtype, device=DEV)
+    print(f"masked logits explicit {dtype}", flush=True)
+    greedy.greedy_candidates(logits, metadata(active), scores, ids, ws, width=width, vocab_start=start,
+                             token_mask=mask, masked_logits=out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(out), want)
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_i)
+    np.testing.assert_array_equal(bits(scores), want_s)
+    # consumed in place: active rows masked, the other rows untouched
+    before = bits(logits).copy()
+    print(f"masked logits consumed {dtype}", flush=True)
+    greedy.greedy_candidates(logits, metadata(active), scores, ids, ws, width=width, vocab_start=start,
+                             token_mask=mask, consume_logits=True)
+    torch.cuda.synchronize()
+    after = bits(logits)
+    np.testing.assert_array_equal(after[:active], want[:active])
+    np.testing.assert_array_equal(after[active:], before[active:])
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_i)
+    # refused operands, before any launch
+    with pytest.raises(TensorParallelSamplingError, match="consumption"):
+        greedy.greedy_candidates(logits, metadata(active), scores, ids, ws, width=width, consume_logits=True)
+    with pytest.raises(TensorParallelSamplingError, match="masked logits"):
+        greedy.greedy_candidates(logits, metadata(active), scores, ids, ws, width=width, vocab_start=start,
+                                 token_mask=mask, masked_logits=torch.empty((rows, width - 1), dtype=dtype, device=DEV))
+    with pytest.raises(TensorParallelSamplingError, match="masked logits"):
+        greedy.greedy_candidates(logits, metadata(active), scores, ids, ws, width=width, vocab_start=start,
+                                 token_mask=mask, masked_logits=logits)                # aliases without consuming
+
+
+def test_captured_sampler_writes_masked_logits(oracle):
+    """CapturedGreedySampler(token_mask=, masked_logits=) (greedy.py:49-69):
+    every replay rewrites the masked logits for the count it runs."""
+    dtype, capacity, width = torch.bfloat16, 4, 3000
+    gen = torch.Generator().manual_seed(22)
+    logits = tie_logits(capacity, width, dtype, gen)
+    mask = torch.randint(-2**31, 2**31, (capacity, (width + 31) // 32), generator=gen,
+                         dtype=torch.int64).to(torch.int32).to(DEV)
+    out = torch.empty((capacity, width), dtype=dtype, device=DEV)
+    ws = ShardedSamplingWorkspace(torch.empty((capacity, 20), dtype=dtype, device=DEV),
+                                  torch.empty((capacity, 20), dtype=torch.int64, device=DEV), None, None)
+    plan = CapturedGreedySampler(local_logits=logits, true_vocab_size=width,
+                                 token_ids=torch.empty(capacity, dtype=torch.int64, device=DEV),
+                                 parameters=params(capacity), workspace=ws,
+                                 root_valid=torch.empty(capacity, dtype=torch.bool, device=DEV),
+                                 token_mask=mask, masked_logits=out)
+    try:
+        for count in (3, 1, 4):
+            print(f"captured masked logits count={count}", flush=True)
+            out.fill_(1.0)
+            plan.replay(count, False)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(bits(out), _expected_masked(bits(logits), mask, 0, count, 0xFF80))
+    finally:
+        plan.close()
